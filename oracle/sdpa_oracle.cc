@@ -1,0 +1,342 @@
+// sdpa_oracle.cc -- TEST INFRASTRUCTURE ONLY.
+//
+// A TensorFlow-free C++ restatement of the reference CPU path for the Sdpa /
+// SdpaGrad ops.  It is the parity checker for the HIP kernels and the timed
+// CPU baseline in bench.py; nothing in the product links it.  Only tests/,
+// __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+//
+// What it follows (paths relative to the reference repository):
+//   rng_bits / rng_uniform   sdpa/sdpa_cpu.cc:198-211  (= sdpa/sdpa_utils.cuh:13-19, test.py:33-46)
+//   fwd_batch                sdpa/sdpa_cpu.cc:213-320  (element-wise online softmax)
+//   bwd_batch                sdpa/sdpa_cpu.cc:322-457  (single pass per (i, j))
+//   batch sharding           sdpa/sdpa_cpu.cc:316-318, 453-455 (parallel over B)
+//
+// Element semantics are a template parameter:
+//   F32   -- T = float.
+//   F16   -- T = Eigen::half as the reference CPU kernel sees it: a product of
+//            two halves is rounded to half before the fp32 add
+//            (sdpa_cpu.cc:261,363,378,424) and dK/dV are read-modify-written in
+//            half once per query row (sdpa_cpu.cc:416-417,437-438).
+// The "gating" oracle for fp16 inputs is the F32 instantiation fed the
+// fp16-exact values (callers widen the inputs and round the outputs); the
+// faithful F16 instantiation is kept for reporting.
+//
+// `gpu_gates` switches the two thresholds where the reference GPU kernels
+// differ from its CPU functors: dropout is active iff p > 1e-6
+// (sdpa_fwd.cu.cc:136, sdpa_bwd.cu.cc:135,296) instead of p > 0
+// (sdpa_cpu.cc:274,391), and the backward skips an element iff P <= 1e-6
+// (sdpa_bwd.cu.cc:131,292) instead of P < 1e-6 (sdpa_cpu.cc:384).
+//
+// Parity status: the RNG, thresholds, epsilons and loop structure are pinned
+// by the tests in tests/test_oracle.py (closed-form known answers, float64
+// brute-force attention, finite differences).  The ulp behaviour of the
+// reference's Eigen::numext::exp/log is not available here (TensorFlow's Eigen
+// is not vendored), so results agree with the reference to rounding only:
+// parity unpinned at the ulp level, absorbed by the stated tolerances.
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+namespace {
+
+// ---- IEEE binary16 <-> binary32, round to nearest even --------------------
+inline float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t mant = h & 0x3ffu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {  // subnormal: renormalise
+            int e = -1;
+            do { ++e; mant <<= 1; } while ((mant & 0x400u) == 0);
+            mant &= 0x3ffu;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+        }
+    } else if (exp == 0x1f) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + (127 - 15)) << 23) | (mant << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+inline uint16_t float_to_half(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t absx = x & 0x7fffffffu;
+    if (absx >= 0x7f800000u) {  // inf or nan
+        return sign | 0x7c00u | (absx > 0x7f800000u ? 0x200u : 0u);
+    }
+    if (absx >= 0x477ff000u) return sign | 0x7c00u;  // rounds to >= 65520 -> inf
+    const int e = (int)(absx >> 23) - 127;
+    if (e < -25) return sign;                          // below half of min subnormal
+    if (e < -14) {  // subnormal half: value / 2^-24, rounded
+        const uint32_t mant = (absx & 0x7fffffu) | 0x800000u;  // 24-bit significand
+        const int shift = -1 - e;                               // 14..24
+        uint32_t q = mant >> shift;
+        const uint32_t rem = mant & ((1u << shift) - 1u), halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (q & 1u))) ++q;  // may carry into the exponent
+        return sign | (uint16_t)q;
+    }
+    // normal half: keep the top 10 fraction bits, round on the 13 dropped ones
+    uint32_t out = ((uint32_t)(e + 15) << 10) | ((absx & 0x7fffffu) >> 13);
+    const uint32_t rem = absx & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (out & 1u))) ++out;  // carry into exponent is correct
+    return sign | (uint16_t)out;
+}
+
+// ---- element semantics ------------------------------------------------------
+struct F32 {
+    using storage = float;
+    static float load(const float* p, size_t i) { return p[i]; }
+    static float mul(float a, float b) { return a * b; }
+    static float round(float x) { return x; }
+    static void store(float* p, size_t i, float x) { p[i] = x; }
+};
+
+struct F16 {
+    using storage = uint16_t;
+    static float load(const uint16_t* p, size_t i) { return half_to_float(p[i]); }
+    // Eigen::half * Eigen::half: exact fp32 product rounded to half.
+    static float mul(float a, float b) { return half_to_float(float_to_half(a * b)); }
+    static float round(float x) { return half_to_float(float_to_half(x)); }
+    static void store(uint16_t* p, size_t i, float x) { p[i] = float_to_half(x); }
+};
+
+constexpr float kEps = 1e-6f;     // sdpa_cpu.cc:230,341
+constexpr float kNegInf = -1e9f;  // sdpa_cpu.cc:227
+
+// sdpa_cpu.cc:198-211
+inline uint32_t rng_bits_impl(uint64_t seed, uint64_t offset, int64_t b, int i, int j,
+                              int stride_m, int stride_n) {
+    const uint64_t batch_stride = (uint64_t)stride_m * (uint64_t)stride_n;
+    const uint64_t idx = (uint64_t)b * batch_stride + (uint64_t)i * (uint64_t)stride_n + (uint64_t)j;
+    const uint64_t global_idx = offset + idx;
+    uint64_t state = seed + global_idx;
+    state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+    return (uint32_t)((state >> 32) & 0xFFFFFFFFu);
+}
+
+inline float rng_uniform_impl(uint64_t seed, uint64_t offset, int64_t b, int i, int j,
+                              int stride_m, int stride_n) {
+    return static_cast<float>(rng_bits_impl(seed, offset, b, i, j, stride_m, stride_n)) /
+           4294967296.0f;
+}
+
+struct Shape {
+    int B, S_q, S_kv, D_qk, D_v;
+};
+
+template <typename T>
+void fwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
+               const typename T::storage* K, const typename T::storage* V,
+               typename T::storage* Out, float* stats, bool causal, float dropout, float scale,
+               uint64_t seed, uint64_t offset, bool gpu_gates) {
+    const bool use_dropout = gpu_gates ? (dropout > kEps) : (dropout > 0.0f);
+    const float dp_inverse_scale = use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
+    std::vector<float> acc(s.D_v);
+    const size_t qb = (size_t)b * s.S_q, kb = (size_t)b * s.S_kv;
+    for (int i = 0; i < s.S_q; ++i) {
+        float m_i = kNegInf;
+        float l_i = 0.0f;
+        std::fill(acc.begin(), acc.end(), 0.0f);
+        for (int j = 0; j < s.S_kv; ++j) {
+            if (causal && j > i) continue;  // sdpa_cpu.cc:253
+            float score = 0.0f;
+            for (int k = 0; k < s.D_qk; ++k) {
+                score += T::mul(T::load(Q, (qb + i) * s.D_qk + k), T::load(K, (kb + j) * s.D_qk + k));
+            }
+            score *= scale;
+            const float m_prev = m_i;
+            m_i = (score > m_prev) ? score : m_prev;
+            const float ratio_prev = std::exp(m_prev - m_i);
+            const float ratio_curr_l = std::exp(score - m_i);
+            float ratio_curr_o = ratio_curr_l;
+            if (use_dropout) {  // sdpa_cpu.cc:274-285
+                if (rng_uniform_impl(seed, offset, b, i, j, s.S_q, s.S_kv) < dropout)
+                    ratio_curr_o = 0.0f;
+                else
+                    ratio_curr_o *= dp_inverse_scale;
+            }
+            l_i = l_i * ratio_prev + ratio_curr_l;  // undropped denominator, sdpa_cpu.cc:287
+            for (int k = 0; k < s.D_v; ++k) {
+                acc[k] *= ratio_prev;
+                acc[k] += T::load(V, (kb + j) * s.D_v + k) * ratio_curr_o;
+            }
+        }
+        stats[qb + i] = m_i + std::log(l_i + kEps);  // sdpa_cpu.cc:302
+        const float inv_l = (l_i > kEps) ? (1.0f / l_i) : 0.0f;
+        for (int k = 0; k < s.D_v; ++k) T::store(Out, (qb + i) * s.D_v + k, acc[k] * inv_l);
+    }
+}
+
+template <typename T>
+void bwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
+               const typename T::storage* K, const typename T::storage* V,
+               const typename T::storage* Out, const float* Stats,
+               const typename T::storage* dO, typename T::storage* dQ, typename T::storage* dK,
+               typename T::storage* dV, bool causal, float dropout, float scale, uint64_t seed,
+               uint64_t offset, bool gpu_gates, bool accumulate_kv_in_t) {
+    const bool use_dropout = gpu_gates ? (dropout > kEps) : (dropout > 0.0f);
+    const float dp_inverse_scale = use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
+    const size_t qb = (size_t)b * s.S_q, kb = (size_t)b * s.S_kv;
+    // dK/dV running sums.  The reference keeps them in T (sdpa_cpu.cc:416-417,437-438);
+    // with accumulate_kv_in_t=false they stay in fp32 as the reference GPU kernel does
+    // (sdpa_bwd.cu.cc:49-56,159-170) and are rounded once at the end.
+    std::vector<float> dk_acc((size_t)s.S_kv * s.D_qk, 0.0f), dv_acc((size_t)s.S_kv * s.D_v, 0.0f);
+    std::vector<float> dq_acc(s.D_qk);
+    for (int i = 0; i < s.S_q; ++i) {
+        const float stats_val = Stats[qb + i];
+        float D_i = 0.0f;  // sdpa_cpu.cc:360-364
+        for (int k = 0; k < s.D_v; ++k)
+            D_i += T::mul(T::load(dO, (qb + i) * s.D_v + k), T::load(Out, (qb + i) * s.D_v + k));
+        std::fill(dq_acc.begin(), dq_acc.end(), 0.0f);
+        for (int j = 0; j < s.S_kv; ++j) {
+            if (causal && j > i) continue;
+            float score = 0.0f;
+            for (int k = 0; k < s.D_qk; ++k)
+                score += T::mul(T::load(Q, (qb + i) * s.D_qk + k), T::load(K, (kb + j) * s.D_qk + k));
+            score *= scale;
+            float prob = std::exp(score - stats_val);
+            if (gpu_gates ? !(prob > kEps) : (prob < kEps)) continue;  // sdpa_cpu.cc:384-385
+            const float prob_raw = prob;
+            bool is_dropped = false;
+            if (use_dropout) {
+                if (rng_uniform_impl(seed, offset, b, i, j, s.S_q, s.S_kv) < dropout) {
+                    is_dropped = true;
+                    prob = 0.0f;
+                } else {
+                    prob *= dp_inverse_scale;
+                }
+            }
+            float dS_val;
+            if (is_dropped) {
+                dS_val = -prob_raw * D_i * scale;  // sdpa_cpu.cc:406-409
+            } else {
+                for (int k = 0; k < s.D_v; ++k) {
+                    float& a = dv_acc[(size_t)j * s.D_v + k];
+                    a = a + prob * T::load(dO, (qb + i) * s.D_v + k);
+                    if (accumulate_kv_in_t) a = T::round(a);
+                }
+                float dP_val = 0.0f;
+                for (int k = 0; k < s.D_v; ++k)
+                    dP_val += T::mul(T::load(dO, (qb + i) * s.D_v + k), T::load(V, (kb + j) * s.D_v + k));
+                dS_val = prob * (dP_val - D_i / dp_inverse_scale) * scale;  // sdpa_cpu.cc:428
+            }
+            for (int k = 0; k < s.D_qk; ++k) {
+                float& a = dk_acc[(size_t)j * s.D_qk + k];
+                a = a + dS_val * T::load(Q, (qb + i) * s.D_qk + k);
+                if (accumulate_kv_in_t) a = T::round(a);
+                dq_acc[k] += dS_val * T::load(K, (kb + j) * s.D_qk + k);
+            }
+        }
+        for (int k = 0; k < s.D_qk; ++k) T::store(dQ, (qb + i) * s.D_qk + k, dq_acc[k]);
+    }
+    for (size_t x = 0; x < (size_t)s.S_kv * s.D_qk; ++x) T::store(dK, kb * s.D_qk + x, dk_acc[x]);
+    for (size_t x = 0; x < (size_t)s.S_kv * s.D_v; ++x) T::store(dV, kb * s.D_v + x, dv_acc[x]);
+}
+
+// Shard [0, B) over `nthreads` threads in contiguous ranges (the reference uses
+// Eigen's parallelFor over the batch, sdpa_cpu.cc:316-318).
+template <typename F>
+void parallel_over_batch(int B, int nthreads, F fn) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > B) nthreads = B;
+    if (nthreads <= 1) {
+        for (int64_t b = 0; b < B; ++b) fn(b);
+        return;
+    }
+    std::vector<std::thread> pool;
+    pool.reserve(nthreads);
+    for (int t = 0; t < nthreads; ++t) {
+        const int64_t lo = (int64_t)B * t / nthreads, hi = (int64_t)B * (t + 1) / nthreads;
+        pool.emplace_back([=] { for (int64_t b = lo; b < hi; ++b) fn(b); });
+    }
+    for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t oracle_rng_bits(uint64_t seed, uint64_t offset, int64_t b, int i, int j, int S_q, int S_kv) {
+    return rng_bits_impl(seed, offset, b, i, j, S_q, S_kv);
+}
+
+float oracle_rng_uniform(uint64_t seed, uint64_t offset, int64_t b, int i, int j, int S_q, int S_kv) {
+    return rng_uniform_impl(seed, offset, b, i, j, S_q, S_kv);
+}
+
+// keep[b, i, j] = 1 unless the reference drops (b, i, j): u < p with u from the
+// float expression of sdpa_cpu.cc:210 (the float predicate, not an integer threshold).
+void oracle_keep_mask(int B, int S_q, int S_kv, float dropout, uint64_t seed, uint64_t offset,
+                      uint8_t* keep, int nthreads) {
+    parallel_over_batch(B, nthreads, [&](int64_t b) {
+        uint8_t* kb = keep + (size_t)b * S_q * S_kv;
+        for (int i = 0; i < S_q; ++i)
+            for (int j = 0; j < S_kv; ++j)
+                kb[(size_t)i * S_kv + j] = rng_uniform_impl(seed, offset, b, i, j, S_q, S_kv) < dropout ? 0 : 1;
+    });
+}
+
+uint16_t oracle_float_to_half(float f) { return float_to_half(f); }
+float oracle_half_to_float(uint16_t h) { return half_to_float(h); }
+
+// dtype: 0 = fp32, 1 = fp16 (faithful Eigen::half semantics).
+int oracle_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* stats,
+                    int B, int S_q, int S_kv, int D_qk, int D_v, int causal, float dropout,
+                    float scale, uint64_t seed, uint64_t offset, int gpu_gates, int nthreads) {
+    const Shape s{B, S_q, S_kv, D_qk, D_v};
+    if (dtype == 0) {
+        parallel_over_batch(B, nthreads, [&](int64_t b) {
+            fwd_batch<F32>(b, s, (const float*)q, (const float*)k, (const float*)v, (float*)o, stats,
+                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0);
+        });
+    } else if (dtype == 1) {
+        parallel_over_batch(B, nthreads, [&](int64_t b) {
+            fwd_batch<F16>(b, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                           (uint16_t*)o, stats, causal != 0, dropout, scale, seed, offset,
+                           gpu_gates != 0);
+        });
+    } else {
+        return 1;
+    }
+    return 0;
+}
+
+// accumulate_kv_in_t: 1 reproduces the reference CPU kernel's per-row rounding of
+// dK/dV to T; 0 accumulates them in fp32 (as the reference GPU kernels do).
+int oracle_sdpa_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
+                    const float* stats, const void* d_o, void* dq, void* dk, void* dv, int B,
+                    int S_q, int S_kv, int D_qk, int D_v, int causal, float dropout, float scale,
+                    uint64_t seed, uint64_t offset, int gpu_gates, int accumulate_kv_in_t,
+                    int nthreads) {
+    const Shape s{B, S_q, S_kv, D_qk, D_v};
+    if (dtype == 0) {
+        parallel_over_batch(B, nthreads, [&](int64_t b) {
+            bwd_batch<F32>(b, s, (const float*)q, (const float*)k, (const float*)v, (const float*)o,
+                           stats, (const float*)d_o, (float*)dq, (float*)dk, (float*)dv,
+                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0, false);
+        });
+    } else if (dtype == 1) {
+        parallel_over_batch(B, nthreads, [&](int64_t b) {
+            bwd_batch<F16>(b, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                           (const uint16_t*)o, stats, (const uint16_t*)d_o, (uint16_t*)dq,
+                           (uint16_t*)dk, (uint16_t*)dv, causal != 0, dropout, scale, seed, offset,
+                           gpu_gates != 0, accumulate_kv_in_t != 0);
+        });
+    } else {
+        return 1;
+    }
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,172 @@
+"""GPU parity of the HIP Sdpa / SdpaGrad kernels against the CPU oracle
+(restatement of sdpa/sdpa_cpu.cc), through the C ABI.
+
+Gates (north_star): fp32 o/grads within 1e-5 max-abs; fp16 o within 2e-3 and
+gradients within 1e-2 of the oracle instantiated in fp32 on the fp16-exact
+inputs; dropout masks bit-exact (test_dropout_gpu.py)."""
+import numpy as np
+import pytest
+import torch
+
+from _common import (CONFIGS, TOL, Cfg, argmax_grad, make_inputs, maxabs, np_dtype, oracle_kw,
+                     sub_batches)
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def run_and_check(pkg, O, c: Cfg, inputs=None, check_faithful=False):
+    q, k, v, d_o = inputs if inputs is not None else make_inputs(c)
+    tol = TOL[c.dtype]
+    kw = dict(dropout=c.dropout, scale=c.scale, causal_mask=c.causal)
+    print(f"[case] {c.name} dtype={c.dtype} B={c.B} S_q={c.S_q} S_kv={c.S_kv} D_qk={c.D_qk} "
+          f"D_v={c.D_v} causal={c.causal} p={c.dropout}", flush=True)
+    o, s = pkg.sdpa(_t(q), _t(k), _t(v), c.seed, c.offset, **kw)
+    torch.cuda.synchronize()
+    o_h, s_h = _np(o), _np(s)
+    if c.do_kind == "argmax":
+        o_ref_full, _ = O.sdpa_fwd_gate(q, k, v, **oracle_kw(c))
+        d_o = argmax_grad(o_ref_full)
+    dq, dk, dv = pkg.sdpa_grad(_t(q), _t(k), _t(v), o, s, _t(d_o), c.seed, c.offset, **kw)
+    torch.cuda.synchronize()
+    dq_h, dk_h, dv_h = _np(dq), _np(dk), _np(dv)
+    assert np.isfinite(o_h.astype(np.float32)).all() and np.isfinite(s_h).all()
+
+    batches = list(c.check_batches) or [None]
+    errs = {"o": 0.0, "stats": 0.0, "dq": 0.0, "dk": 0.0, "dv": 0.0}
+    for bsel in batches:
+        sel = (lambda a: a) if bsel is None else (lambda a, b=bsel: a[b:b + 1])
+        b0 = 0 if bsel is None else bsel
+        okw = oracle_kw(c, b0)
+        o_ref, s_ref = O.sdpa_fwd_gate(sel(q), sel(k), sel(v), **okw)
+        # The backward is checked on the kernel's own o/stats (as the op is used).
+        g_ref = O.sdpa_bwd_gate(sel(q), sel(k), sel(v), sel(o_h), sel(s_h), sel(d_o), **okw)
+        errs["o"] = max(errs["o"], maxabs(sel(o_h), o_ref))
+        errs["stats"] = max(errs["stats"], maxabs(sel(s_h), s_ref))
+        for name, got, ref in zip(("dq", "dk", "dv"), (dq_h, dk_h, dv_h), g_ref):
+            errs[name] = max(errs[name], maxabs(sel(got), ref))
+    print(f"[errs] {c.name}: " + " ".join(f"{k}={v:.3e}" for k, v in errs.items()), flush=True)
+    assert errs["o"] <= tol["o"], errs
+    assert errs["stats"] <= tol["stats"], errs
+    for name in ("dq", "dk", "dv"):
+        assert errs[name] <= tol["grad"], errs
+    return errs
+
+
+@pytest.mark.parametrize("c", CONFIGS, ids=[c.name for c in CONFIGS])
+def test_baseline_config(pkg, O, c):
+    run_and_check(pkg, O, c)
+
+
+EDGE = [
+    # dtype, B, S_q, S_kv, D_qk, D_v, causal, dropout
+    ("f16", 2, 1, 1, 8, 8, False, 0.0),
+    ("f16", 3, 77, 77, 64, 64, True, 0.0),
+    ("f16", 2, 129, 200, 128, 128, False, 0.3),
+    ("f16", 2, 300, 300, 128, 128, True, 0.1),
+    ("f16", 2, 65, 130, 16, 48, False, 0.0),
+    ("f16", 2, 33, 257, 100, 36, False, 0.05),
+    ("f16", 1, 50, 50, 1, 1, True, 0.0),
+    ("f16", 2, 96, 64, 128, 8, False, 0.5),
+    ("f16", 2, 64, 96, 40, 128, False, 0.0),
+    ("f32", 2, 1, 1, 8, 8, False, 0.0),
+    ("f32", 3, 77, 77, 64, 64, True, 0.0),
+    ("f32", 2, 129, 200, 128, 128, False, 0.3),
+    ("f32", 2, 300, 300, 128, 64, True, 0.1),
+    ("f32", 2, 65, 130, 16, 48, False, 0.0),
+    ("f32", 2, 33, 257, 100, 36, False, 0.05),
+    ("f32", 1, 50, 50, 1, 3, True, 0.0),
+    ("f32", 2, 96, 64, 128, 8, False, 0.5),
+]
+
+
+@pytest.mark.parametrize("case", EDGE, ids=["-".join(map(str, e)) for e in EDGE])
+def test_edge_shapes(pkg, O, case):
+    dt, B, S_q, S_kv, D_qk, D_v, causal, p = case
+    c = Cfg(f"edge_{dt}_{B}x{S_q}x{S_kv}_{D_qk}_{D_v}", dt, B, S_q, S_kv, D_qk, D_v, causal, p,
+            D_qk ** -0.5 if D_qk else 1.0, seed=11, offset=5)
+    run_and_check(pkg, O, c)
+
+
+def test_unaligned_pointers_take_scalar_path(pkg, O):
+    """Views starting 2 elements into a buffer are not 16-byte aligned: the
+    kernels fall back to element loads/stores and must agree."""
+    c = Cfg("unaligned", "f16", 2, 70, 70, 64, 64, True, 0.2, 0.125, 3, 9)
+    q, k, v, d_o = make_inputs(c)
+    def shifted(a):
+        buf = torch.empty(a.size + 2, dtype=torch.float16, device=DEV)
+        view = buf[2:].view(a.shape)
+        view.copy_(_t(a))
+        return view
+    kw = dict(dropout=c.dropout, scale=c.scale, causal_mask=c.causal)
+    o1, s1 = pkg.sdpa(shifted(q), shifted(k), shifted(v), c.seed, c.offset, **kw)
+    o2, s2 = pkg.sdpa(_t(q), _t(k), _t(v), c.seed, c.offset, **kw)
+    torch.cuda.synchronize()
+    assert maxabs(_np(o1), _np(o2)) <= 1e-3
+    assert maxabs(_np(s1), _np(s2)) <= 1e-5
+    g1 = pkg.sdpa_grad(shifted(q), shifted(k), shifted(v), shifted(_np(o2)), s2, shifted(d_o),
+                       c.seed, c.offset, **kw)
+    g2 = pkg.sdpa_grad(_t(q), _t(k), _t(v), o2, s2, _t(d_o), c.seed, c.offset, **kw)
+    torch.cuda.synchronize()
+    for a, b in zip(g1, g2):
+        assert maxabs(_np(a), _np(b)) <= 5e-3
+
+
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+def test_repeat_runs_bitwise_identical(pkg, dt):
+    """Determinism (reference test.py:176-179): no atomics, fixed reduction order."""
+    c = Cfg("det", dt, 4, 512, 512, 128, 128, True, 0.1, 128 ** -0.5, 7, 0)
+    q, k, v, d_o = (_t(a) for a in make_inputs(c))
+    kw = dict(dropout=c.dropout, scale=c.scale, causal_mask=c.causal)
+    ref = None
+    for _ in range(3):
+        o, s = pkg.sdpa(q, k, v, c.seed, c.offset, **kw)
+        g = pkg.sdpa_grad(q, k, v, o, s, d_o, c.seed, c.offset, **kw)
+        outs = [_np(t).tobytes() for t in (o, s, *g)]
+        if ref is None:
+            ref = outs
+        assert outs == ref
+
+
+def test_autograd_function_matches_ops(pkg):
+    c = Cfg("autograd", "f16", 2, 128, 128, 64, 64, True, 0.1, 0.125, 42, 1000)
+    q, k, v, d_o = (_t(a) for a in make_inputs(c))
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o, s = pkg.sdpa_autograd(qa, ka, va, c.seed, c.offset, c.dropout, c.scale, c.causal)
+    o.backward(d_o)
+    o2, s2 = pkg.sdpa(q, k, v, c.seed, c.offset, dropout=c.dropout, scale=c.scale, causal_mask=True)
+    g2 = pkg.sdpa_grad(q, k, v, o2, s2, d_o, c.seed, c.offset, dropout=c.dropout, scale=c.scale,
+                       causal_mask=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(s, s2)
+    for a, b in zip((qa.grad, ka.grad, va.grad), g2):
+        assert torch.equal(a, b)
+
+
+def test_empty_inputs(pkg):
+    """Zero-sized batch/sequence: no launch, no error (the reference would fail
+    its launch check on an empty grid)."""
+    for shape in [(0, 16, 16, 8, 8), (2, 0, 16, 8, 8), (2, 16, 0, 8, 8)]:
+        B, S_q, S_kv, D_qk, D_v = shape
+        q = torch.zeros((B, S_q, D_qk), dtype=torch.float16, device=DEV)
+        k = torch.zeros((B, S_kv, D_qk), dtype=torch.float16, device=DEV)
+        v = torch.zeros((B, S_kv, D_v), dtype=torch.float16, device=DEV)
+        o, s = pkg.sdpa(q, k, v, 0, 0)
+        dq, dk, dv = pkg.sdpa_grad(q, k, v, o, s, torch.zeros_like(o), 0, 0)
+        torch.cuda.synchronize()
+        assert o.shape == (B, S_q, D_v) and dq.shape == q.shape and dk.shape == k.shape
+        if S_kv == 0 and B * S_q:
+            # no keys: o = 0 and stats = -1e9 + log(1e-6) (sdpa_cpu.cc:302-308)
+            assert torch.all(o == 0)
+            assert torch.all(s == np.float32(-1e9) + np.float32(np.log(np.float32(1e-6))))
+        if S_q == 0 and B * S_kv:
+            assert torch.all(dk == 0) and torch.all(dv == 0)

@@ -1,0 +1,236 @@
+// sdpa_capi.hip -- the extern "C" entry points declared in include/sdpa_hip.h:
+// argument validation with the reference's messages, the dropout threshold,
+// and dispatch to the forward / backward launchers.
+#include <math.h>
+#include <stdint.h>
+
+#include "sdpa_hip.h"
+#include "sdpa_device.h"
+#include "sdpa_launch.h"
+#include "sdpa_params.h"
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+int hip_status(hipError_t e) {
+    if (e == hipSuccess) return SDPA_OK;
+    g_last_hip_error = (int)e;
+    return SDPA_ERR_HIP;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+// Smallest uint32 value v with (float)v / 2^32 >= p, as a 64-bit number
+// (2^32 if none).  (float)v rounds to nearest even, which is monotone in v,
+// so "u < p" is the prefix v < T(p) of the 32-bit range.  T(p) is not
+// floor(p * 2^32): e.g. T(0.1f) = 0x19999991, T(0.2f) = 0x33333321.
+uint64_t drop_threshold_impl(float p) {
+    if (!(p > 0.0f)) return 0;  // nothing satisfies u < p (also NaN)
+    const float P = p * 4294967296.0f;  // exact: scaling by a power of two
+    if (!((float)4294967295u >= P)) return 1ull << 32;
+    uint64_t lo = 0, hi = 0xFFFFFFFFull;
+    while (lo < hi) {
+        const uint64_t mid = (lo + hi) >> 1;
+        if ((float)(uint32_t)mid >= P) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
+// Host-side derivation of the per-call constants (reference:
+// dp_inverse = 1 / (1 - p) when p > EPSF, sdpa/sdpa_fwd.cu.cc:20).
+sdpa::AttnScalars make_scalars(float scale, float dropout, int causal, uint64_t seed, uint64_t offset) {
+    sdpa::AttnScalars c{};
+    c.scale = scale;
+    c.scale_log2 = scale * sdpa::kLog2e;
+    c.use_dropout = dropout > sdpa::kEps ? 1 : 0;
+    c.keep_scale = c.use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
+    c.drop_threshold = c.use_dropout ? (uint32_t)drop_threshold_impl(dropout) : 0u;
+    c.causal = causal ? 1 : 0;
+    c.seed_offset = seed + offset;
+    return c;
+}
+
+int check_common(int dtype, int B, int S_q, int S_kv, int D_qk, int D_v, float dropout, int causal) {
+    if (dtype != SDPA_DTYPE_F32 && dtype != SDPA_DTYPE_F16) return SDPA_ERR_DTYPE;
+    if (B < 0 || S_q < 0 || S_kv < 0 || D_qk < 0 || D_v < 0) return SDPA_ERR_NEGATIVE_DIM;
+    if (causal && S_q != S_kv) return SDPA_ERR_CAUSAL_SEQ;
+    if ((D_qk > D_v ? D_qk : D_v) > 128) return SDPA_ERR_FEATURE_TOO_LARGE;
+    if (!(dropout < 1.0f) && !isnan(dropout)) return SDPA_ERR_DROPOUT_RANGE;
+    return SDPA_OK;
+}
+
+bool vec_ok(int dtype, int D_qk, int D_v, std::initializer_list<const void*> ptrs) {
+    const int w = dtype == SDPA_DTYPE_F16 ? 8 : 4;  // elements per 16-byte chunk
+    if (D_qk % w != 0 || D_v % w != 0) return false;
+    for (const void* p : ptrs)
+        if (!aligned16(p)) return false;
+    return true;
+}
+
+// keep[b, i, j] from the same hash code the attention kernels use.
+__global__ void dropout_mask_kernel(uint8_t* keep, int B, int S_q, int S_kv, int use_dropout,
+                                    uint32_t thr, uint64_t seed_offset) {
+    const uint64_t total = (uint64_t)B * S_q * S_kv;
+    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t row = idx / (uint64_t)S_kv, j = idx % (uint64_t)S_kv;
+        keep[idx] = use_dropout ? (uint8_t)sdpa::lcg_keep(sdpa::lcg_state(seed_offset, row, S_kv, j), thr) : 1;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sdpa_hip_status_string(int status) {
+    switch (status) {
+        case SDPA_OK: return "OK";
+        case SDPA_ERR_SEED_NOT_SCALAR: return "seed must be scalar";
+        case SDPA_ERR_OFFSET_NOT_SCALAR: return "offset must be scalar";
+        case SDPA_ERR_K_BATCH: return "K batch size mismatch";
+        case SDPA_ERR_K_FEATURE: return "K feature size mismatch";
+        case SDPA_ERR_V_BATCH: return "V batch size mismatch";
+        case SDPA_ERR_V_SEQ: return "V seq size mismatch";
+        case SDPA_ERR_O_BATCH: return "O batch size mismatch";
+        case SDPA_ERR_O_SEQ: return "O seq size mismatch";
+        case SDPA_ERR_O_FEATURE: return "O feature size mismatch";
+        case SDPA_ERR_DO_BATCH: return "dO batch size mismatch";
+        case SDPA_ERR_DO_SEQ: return "dO seq size mismatch";
+        case SDPA_ERR_DO_FEATURE: return "dO feature size mismatch";
+        case SDPA_ERR_S_BATCH: return "S batch size mismatch";
+        case SDPA_ERR_S_SEQ: return "S seq size mismatch";
+        case SDPA_ERR_CAUSAL_SEQ: return "seq size Q != K while causal_mask = True";
+        case SDPA_ERR_FEATURE_TOO_LARGE:
+            return "CUDA kernel does not support feature size over 128. Set smaller feature size or "
+                   "use more heads";
+        case SDPA_ERR_RANK: return "Shape must be rank 3";
+        case SDPA_ERR_DTYPE: return "dtype must be float16 or float32";
+        case SDPA_ERR_NEGATIVE_DIM: return "tensor dimensions must be non-negative";
+        case SDPA_ERR_NULL_POINTER: return "null device pointer for a non-empty tensor";
+        case SDPA_ERR_DROPOUT_RANGE: return "dropout must be < 1";
+        case SDPA_ERR_WORKSPACE: return "backward workspace is too small";
+        case SDPA_ERR_HIP: return "HIP runtime error";
+        default: return "unknown sdpa status";
+    }
+}
+
+int sdpa_hip_last_hip_error(void) { return g_last_hip_error; }
+
+int sdpa_hip_check_fwd(int q_rank, const int64_t* q, int k_rank, const int64_t* k, int v_rank,
+                       const int64_t* v, int seed_rank, int offset_rank, int causal_mask) {
+    if (q_rank != 3 || k_rank != 3 || v_rank != 3) return SDPA_ERR_RANK;  // sdpa_ops.cc:22-25
+    if (seed_rank != 0) return SDPA_ERR_SEED_NOT_SCALAR;                  // sdpa_cpu.cc:37-40
+    if (offset_rank != 0) return SDPA_ERR_OFFSET_NOT_SCALAR;
+    if (k[0] != q[0]) return SDPA_ERR_K_BATCH;  // sdpa_cpu.cc:51-58
+    if (k[2] != q[2]) return SDPA_ERR_K_FEATURE;
+    if (v[0] != q[0]) return SDPA_ERR_V_BATCH;
+    if (v[1] != k[1]) return SDPA_ERR_V_SEQ;
+    if (causal_mask && q[1] != k[1]) return SDPA_ERR_CAUSAL_SEQ;      // :60-64
+    if ((q[2] > v[2] ? q[2] : v[2]) > 128) return SDPA_ERR_FEATURE_TOO_LARGE;  // :66-69
+    return SDPA_OK;
+}
+
+int sdpa_hip_check_bwd(int q_rank, const int64_t* q, int k_rank, const int64_t* k, int v_rank,
+                       const int64_t* v, int o_rank, const int64_t* o, int stats_rank,
+                       const int64_t* st, int do_rank, const int64_t* d_o, int seed_rank,
+                       int offset_rank, int causal_mask) {
+    if (q_rank != 3 || k_rank != 3 || v_rank != 3) return SDPA_ERR_RANK;  // sdpa_ops.cc:55-57
+    if (seed_rank != 0) return SDPA_ERR_SEED_NOT_SCALAR;                  // sdpa_cpu.cc:116-119
+    if (offset_rank != 0) return SDPA_ERR_OFFSET_NOT_SCALAR;
+    // The reference indexes dim_size(0..2) of out/do and (0..1) of stats;
+    // a tensor of lower rank has no such dimension and fails the same check.
+    auto dim = [](int rank, const int64_t* s, int i) -> int64_t { return i < rank ? s[i] : -1; };
+    if (k[0] != q[0]) return SDPA_ERR_K_BATCH;  // sdpa_cpu.cc:130-133
+    if (k[2] != q[2]) return SDPA_ERR_K_FEATURE;
+    if (v[0] != q[0]) return SDPA_ERR_V_BATCH;  // :135-138
+    if (v[1] != k[1]) return SDPA_ERR_V_SEQ;
+    if (dim(o_rank, o, 0) != q[0]) return SDPA_ERR_O_BATCH;  // :140-145
+    if (dim(o_rank, o, 1) != q[1]) return SDPA_ERR_O_SEQ;
+    if (dim(o_rank, o, 2) != v[2]) return SDPA_ERR_O_FEATURE;
+    if (dim(do_rank, d_o, 0) != q[0]) return SDPA_ERR_DO_BATCH;  // :147-152
+    if (dim(do_rank, d_o, 1) != q[1]) return SDPA_ERR_DO_SEQ;
+    if (dim(do_rank, d_o, 2) != v[2]) return SDPA_ERR_DO_FEATURE;
+    if (dim(stats_rank, st, 0) != q[0]) return SDPA_ERR_S_BATCH;  // :154-157
+    if (dim(stats_rank, st, 1) != q[1]) return SDPA_ERR_S_SEQ;
+    if (causal_mask && q[1] != k[1]) return SDPA_ERR_CAUSAL_SEQ;  // :159-163
+    if ((q[2] > v[2] ? q[2] : v[2]) > 128) return SDPA_ERR_FEATURE_TOO_LARGE;  // :165-168
+    return SDPA_OK;
+}
+
+int sdpa_hip_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* stats,
+                 int B, int S_q, int S_kv, int D_qk, int D_v, float scale, float dropout,
+                 int causal_mask, uint64_t seed, uint64_t offset, hipStream_t stream) {
+    int st = check_common(dtype, B, S_q, S_kv, D_qk, D_v, dropout, causal_mask);
+    if (st != SDPA_OK) return st;
+    if ((size_t)B * S_q == 0) return SDPA_OK;  // empty grid: nothing to do
+    if (!stats || (D_v > 0 && !o) || (D_qk > 0 && (!q || (S_kv > 0 && !k))) || (S_kv > 0 && D_v > 0 && !v))
+        return SDPA_ERR_NULL_POINTER;
+    sdpa::FwdParams p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.stats = stats;
+    p.s = sdpa::AttnShape{B, S_q, S_kv, D_qk, D_v};
+    p.c = make_scalars(scale, dropout, causal_mask, seed, offset);
+    const bool vec = vec_ok(dtype, D_qk, D_v, {q, k, v, o});
+    return hip_status(sdpa::launch_fwd(p, (sdpa::DType)dtype, vec, stream));
+}
+
+size_t sdpa_hip_bwd_workspace_bytes(int B, int S_q) {
+    if (B <= 0 || S_q <= 0) return 0;
+    const size_t bytes = (size_t)B * (size_t)S_q * sizeof(float);
+    return (bytes + 255) & ~(size_t)255;
+}
+
+int sdpa_hip_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
+                 const float* stats, const void* d_o, void* dq, void* dk, void* dv,
+                 void* workspace, size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk,
+                 int D_v, float scale, float dropout, int causal_mask, uint64_t seed,
+                 uint64_t offset, hipStream_t stream) {
+    int st = check_common(dtype, B, S_q, S_kv, D_qk, D_v, dropout, causal_mask);
+    if (st != SDPA_OK) return st;
+    if (B == 0) return SDPA_OK;
+    if (workspace_bytes < sdpa_hip_bwd_workspace_bytes(B, S_q)) return SDPA_ERR_WORKSPACE;
+    const bool has_q = (size_t)S_q > 0, has_kv = (size_t)S_kv > 0;
+    if ((has_q && (!stats || !workspace)) || (has_q && D_qk > 0 && (!q || !dq)) ||
+        (has_q && D_v > 0 && (!o || !d_o)) || (has_kv && D_qk > 0 && (!k || !dk)) ||
+        (has_kv && D_v > 0 && (!v || !dv)))
+        return SDPA_ERR_NULL_POINTER;
+    sdpa::BwdParams p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.stats = stats;
+    p.d_o = d_o;
+    p.dq = dq;
+    p.dk = dk;
+    p.dv = dv;
+    p.delta = static_cast<float*>(workspace);
+    p.s = sdpa::AttnShape{B, S_q, S_kv, D_qk, D_v};
+    p.c = make_scalars(scale, dropout, causal_mask, seed, offset);
+    const bool vec = vec_ok(dtype, D_qk, D_v, {q, k, v, o, d_o, dq, dk, dv});
+    return hip_status(sdpa::launch_bwd(p, (sdpa::DType)dtype, vec, stream));
+}
+
+uint64_t sdpa_hip_drop_threshold(float dropout) { return drop_threshold_impl(dropout); }
+
+int sdpa_hip_dropout_mask(uint8_t* keep, int B, int S_q, int S_kv, float dropout, uint64_t seed,
+                          uint64_t offset, hipStream_t stream) {
+    if (B < 0 || S_q < 0 || S_kv < 0) return SDPA_ERR_NEGATIVE_DIM;
+    if (!(dropout < 1.0f) && !isnan(dropout)) return SDPA_ERR_DROPOUT_RANGE;
+    const uint64_t total = (uint64_t)B * S_q * S_kv;
+    if (total == 0) return SDPA_OK;
+    if (!keep) return SDPA_ERR_NULL_POINTER;
+    const sdpa::AttnScalars c = make_scalars(1.0f, dropout, 0, seed, offset);
+    const uint64_t blocks = (total + 255) / 256;
+    const unsigned grid = (unsigned)(blocks < 65536 ? blocks : 65536);
+    hipLaunchKernelGGL(dropout_mask_kernel, dim3(grid), dim3(256), 0, stream, keep, B, S_q, S_kv,
+                       c.use_dropout, c.drop_threshold, c.seed_offset);
+    return hip_status(hipGetLastError());
+}
+
+}  // extern "C"

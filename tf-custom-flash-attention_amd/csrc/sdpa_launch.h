@@ -1,0 +1,56 @@
+// sdpa_launch.h -- host-side launch helpers shared by the forward and backward
+// launchers: compile-time dispatch over the padded feature widths and flags,
+// and a launch wrapper that raises the dynamic-LDS limit once per kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <type_traits>
+
+#include "sdpa_params.h"
+
+namespace sdpa {
+
+enum class DType : int { F32 = 0, F16 = 1 };
+
+// Padded feature width for D in [0, 128]: the MFMA tiles are 32 wide in the
+// output direction, so every kernel is instantiated for 32, 64 and 128
+// (the reference buckets max(D_qk, D_v) into 8/16/32/64/128,
+// sdpa/sdpa_fwd.cu.cc:191-215; here D_qk and D_v are bucketed separately).
+template <typename F>
+hipError_t with_dim(int d, F&& f) {
+    if (d <= 32) return f(std::integral_constant<int, 32>{});
+    if (d <= 64) return f(std::integral_constant<int, 64>{});
+    return f(std::integral_constant<int, 128>{});
+}
+
+template <typename F>
+hipError_t with_bool(bool b, F&& f) {
+    if (b) return f(std::true_type{});
+    return f(std::false_type{});
+}
+
+// Launch `kern` with `lds` bytes of dynamic LDS.  The per-kernel attribute is
+// set once per process (gfx950 has 160 KB of LDS per CU; kernels here use at
+// most ~100 KB).
+// The kernel is a template argument so that each kernel gets its own once-flag.
+template <auto kern, typename... Args>
+hipError_t launch_kernel(unsigned grid, unsigned block, size_t lds, hipStream_t stream,
+                         const Args&... args) {
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    std::call_once(once, [&] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    });
+    if (attr_err != hipSuccess) return attr_err;
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(block), lds, stream, args...);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwd(const FwdParams& p, DType dtype, bool vec, hipStream_t stream);
+hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, hipStream_t stream);
+
+}  // namespace sdpa
