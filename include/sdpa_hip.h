@@ -110,6 +110,25 @@ int sdpa_hip_bwd(int dtype, const void* q, const void* k, const void* v, const v
                  int D_v, float scale, float dropout, int causal_mask, uint64_t seed,
                  uint64_t offset, hipStream_t stream);
 
+/* The two launches of sdpa_hip_bwd as separate calls, same arguments, same
+ * stream order required (the reference launches its two backward kernels
+ * back to back, sdpa/sdpa_bwd.cu.cc:402-405):
+ *   sdpa_hip_bwd_dq   -- dQ, and delta into the workspace;
+ *   sdpa_hip_bwd_dkdv -- dK and dV, reading the delta left in the workspace
+ *                        by a preceding sdpa_hip_bwd_dq with the same inputs.
+ * sdpa_hip_bwd == sdpa_hip_bwd_dq followed by sdpa_hip_bwd_dkdv.            */
+int sdpa_hip_bwd_dq(int dtype, const void* q, const void* k, const void* v, const void* o,
+                    const float* stats, const void* d_o, void* dq, void* workspace,
+                    size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
+                    float scale, float dropout, int causal_mask, uint64_t seed, uint64_t offset,
+                    hipStream_t stream);
+
+int sdpa_hip_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, const float* stats,
+                      const void* d_o, void* dk, void* dv, const void* workspace,
+                      size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
+                      float scale, float dropout, int causal_mask, uint64_t seed,
+                      uint64_t offset, hipStream_t stream);
+
 /* ---- dropout hash (sdpa/sdpa_utils.cuh:13-19, sdpa/sdpa_cpu.cc:198-211) ----
  * Integer form of the reference's predicate (float)(st >> 32) / 2^32 < p:
  * element dropped iff (st >> 32) < T(p).  Returns T(p) as a 64-bit value

@@ -51,11 +51,11 @@ def lib():
         L.oracle_half_to_float.argtypes = [ctypes.c_uint16]
         L.oracle_sdpa_fwd.restype = _int
         L.oracle_sdpa_fwd.argtypes = [_int, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _int,
-                                      _int, _flt, _flt, _u64, _u64, _int, _int]
+                                      _int, _flt, _flt, _u64, _u64, _int, _int, _int, _int]
         L.oracle_sdpa_bwd.restype = _int
         L.oracle_sdpa_bwd.argtypes = [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _int,
                                       _int, _int, _int, _int, _int, _flt, _flt, _u64, _u64, _int,
-                                      _int, _int]
+                                      _int, _int, _int, _int]
         _lib = L
     return _lib
 
@@ -94,8 +94,10 @@ def _c(a: np.ndarray) -> np.ndarray:
 
 
 def sdpa_fwd(q, k, v, *, scale=1.0, dropout=0.0, causal_mask=False, seed=0, offset=0,
-             gpu_gates=True, nthreads=None):
-    """Reference forward (sdpa_cpu.cc:213-320). Returns (o [B,S_q,D_v] in q.dtype, stats f32 [B,S_q])."""
+             gpu_gates=True, nthreads=None, rows=None):
+    """Reference forward (sdpa_cpu.cc:213-320). Returns (o [B,S_q,D_v] in q.dtype, stats f32 [B,S_q]).
+
+    rows=(i0, i1) computes only query rows [i0, i1) (a timing sample)."""
     q, k, v = _c(q), _c(k), _c(v)
     assert q.dtype == k.dtype == v.dtype
     B, S_q, D_qk = q.shape
@@ -105,13 +107,14 @@ def sdpa_fwd(q, k, v, *, scale=1.0, dropout=0.0, causal_mask=False, seed=0, offs
     rc = lib().oracle_sdpa_fwd(_dtype_code(q), q.ctypes.data, k.ctypes.data, v.ctypes.data,
                                o.ctypes.data, stats.ctypes.data, B, S_q, S_kv, D_qk, D_v,
                                int(bool(causal_mask)), float(dropout), float(scale), int(seed),
-                               int(offset), int(bool(gpu_gates)), nthreads or default_threads())
+                               int(offset), int(bool(gpu_gates)), nthreads or default_threads(),
+                               *(rows or (0, -1)))
     assert rc == 0
     return o, stats
 
 
 def sdpa_bwd(q, k, v, o, stats, d_o, *, scale=1.0, dropout=0.0, causal_mask=False, seed=0,
-             offset=0, gpu_gates=True, accumulate_kv_in_t=False, nthreads=None):
+             offset=0, gpu_gates=True, accumulate_kv_in_t=False, nthreads=None, rows=None):
     """Reference backward (sdpa_cpu.cc:322-457). Returns (dq, dk, dv) in q.dtype."""
     q, k, v, o, d_o = _c(q), _c(k), _c(v), _c(o), _c(d_o)
     stats = np.ascontiguousarray(stats, dtype=np.float32)
@@ -125,7 +128,7 @@ def sdpa_bwd(q, k, v, o, stats, d_o, *, scale=1.0, dropout=0.0, causal_mask=Fals
                                dk.ctypes.data, dv.ctypes.data, B, S_q, S_kv, D_qk, D_v,
                                int(bool(causal_mask)), float(dropout), float(scale), int(seed),
                                int(offset), int(bool(gpu_gates)), int(bool(accumulate_kv_in_t)),
-                               nthreads or default_threads())
+                               nthreads or default_threads(), *(rows or (0, -1)))
     assert rc == 0
     return dq, dk, dv
 

@@ -139,12 +139,12 @@ template <typename T>
 void fwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
                const typename T::storage* K, const typename T::storage* V,
                typename T::storage* Out, float* stats, bool causal, float dropout, float scale,
-               uint64_t seed, uint64_t offset, bool gpu_gates) {
+               uint64_t seed, uint64_t offset, bool gpu_gates, int row_begin, int row_end) {
     const bool use_dropout = gpu_gates ? (dropout > kEps) : (dropout > 0.0f);
     const float dp_inverse_scale = use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
     std::vector<float> acc(s.D_v);
     const size_t qb = (size_t)b * s.S_q, kb = (size_t)b * s.S_kv;
-    for (int i = 0; i < s.S_q; ++i) {
+    for (int i = row_begin; i < row_end; ++i) {
         float m_i = kNegInf;
         float l_i = 0.0f;
         std::fill(acc.begin(), acc.end(), 0.0f);
@@ -184,7 +184,7 @@ void bwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
                const typename T::storage* Out, const float* Stats,
                const typename T::storage* dO, typename T::storage* dQ, typename T::storage* dK,
                typename T::storage* dV, bool causal, float dropout, float scale, uint64_t seed,
-               uint64_t offset, bool gpu_gates, bool accumulate_kv_in_t) {
+               uint64_t offset, bool gpu_gates, bool accumulate_kv_in_t, int row_begin, int row_end) {
     const bool use_dropout = gpu_gates ? (dropout > kEps) : (dropout > 0.0f);
     const float dp_inverse_scale = use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
     const size_t qb = (size_t)b * s.S_q, kb = (size_t)b * s.S_kv;
@@ -193,7 +193,7 @@ void bwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
     // (sdpa_bwd.cu.cc:49-56,159-170) and are rounded once at the end.
     std::vector<float> dk_acc((size_t)s.S_kv * s.D_qk, 0.0f), dv_acc((size_t)s.S_kv * s.D_v, 0.0f);
     std::vector<float> dq_acc(s.D_qk);
-    for (int i = 0; i < s.S_q; ++i) {
+    for (int i = row_begin; i < row_end; ++i) {
         const float stats_val = Stats[qb + i];
         float D_i = 0.0f;  // sdpa_cpu.cc:360-364
         for (int k = 0; k < s.D_v; ++k)
@@ -291,20 +291,27 @@ uint16_t oracle_float_to_half(float f) { return float_to_half(f); }
 float oracle_half_to_float(uint16_t h) { return half_to_float(h); }
 
 // dtype: 0 = fp32, 1 = fp16 (faithful Eigen::half semantics).
+// Query rows [row_begin, row_end) of every batch are computed (row_end < 0:
+// all rows); the others are left untouched.  A row range is only used to
+// time a bounded sample of a large workload.
 int oracle_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* stats,
                     int B, int S_q, int S_kv, int D_qk, int D_v, int causal, float dropout,
-                    float scale, uint64_t seed, uint64_t offset, int gpu_gates, int nthreads) {
+                    float scale, uint64_t seed, uint64_t offset, int gpu_gates, int nthreads,
+                    int row_begin, int row_end) {
     const Shape s{B, S_q, S_kv, D_qk, D_v};
+    if (row_end < 0 || row_end > S_q) row_end = S_q;
+    if (row_begin < 0) row_begin = 0;
     if (dtype == 0) {
         parallel_over_batch(B, nthreads, [&](int64_t b) {
             fwd_batch<F32>(b, s, (const float*)q, (const float*)k, (const float*)v, (float*)o, stats,
-                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0);
+                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0, row_begin,
+                           row_end);
         });
     } else if (dtype == 1) {
         parallel_over_batch(B, nthreads, [&](int64_t b) {
             fwd_batch<F16>(b, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                            (uint16_t*)o, stats, causal != 0, dropout, scale, seed, offset,
-                           gpu_gates != 0);
+                           gpu_gates != 0, row_begin, row_end);
         });
     } else {
         return 1;
@@ -318,20 +325,23 @@ int oracle_sdpa_bwd(int dtype, const void* q, const void* k, const void* v, cons
                     const float* stats, const void* d_o, void* dq, void* dk, void* dv, int B,
                     int S_q, int S_kv, int D_qk, int D_v, int causal, float dropout, float scale,
                     uint64_t seed, uint64_t offset, int gpu_gates, int accumulate_kv_in_t,
-                    int nthreads) {
+                    int nthreads, int row_begin, int row_end) {
     const Shape s{B, S_q, S_kv, D_qk, D_v};
+    if (row_end < 0 || row_end > S_q) row_end = S_q;
+    if (row_begin < 0) row_begin = 0;
     if (dtype == 0) {
         parallel_over_batch(B, nthreads, [&](int64_t b) {
             bwd_batch<F32>(b, s, (const float*)q, (const float*)k, (const float*)v, (const float*)o,
                            stats, (const float*)d_o, (float*)dq, (float*)dk, (float*)dv,
-                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0, false);
+                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0, false,
+                           row_begin, row_end);
         });
     } else if (dtype == 1) {
         parallel_over_batch(B, nthreads, [&](int64_t b) {
             bwd_batch<F16>(b, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                            (const uint16_t*)o, stats, (const uint16_t*)d_o, (uint16_t*)dq,
                            (uint16_t*)dk, (uint16_t*)dv, causal != 0, dropout, scale, seed, offset,
-                           gpu_gates != 0, accumulate_kv_in_t != 0);
+                           gpu_gates != 0, accumulate_kv_in_t != 0, row_begin, row_end);
         });
     } else {
         return 1;

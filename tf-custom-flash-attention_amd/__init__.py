@@ -76,6 +76,12 @@ def library():
     L.sdpa_hip_bwd.restype = i32
     L.sdpa_hip_bwd.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, i32, i32, i32,
                                i32, i32, f32, f32, i32, u64, u64, vp]
+    L.sdpa_hip_bwd_dq.restype = i32
+    L.sdpa_hip_bwd_dq.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, sz, i32, i32, i32, i32,
+                                  i32, f32, f32, i32, u64, u64, vp]
+    L.sdpa_hip_bwd_dkdv.restype = i32
+    L.sdpa_hip_bwd_dkdv.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, sz, i32, i32, i32, i32,
+                                    i32, f32, f32, i32, u64, u64, vp]
     L.sdpa_hip_drop_threshold.restype = u64
     L.sdpa_hip_drop_threshold.argtypes = [f32]
     L.sdpa_hip_dropout_mask.restype = i32

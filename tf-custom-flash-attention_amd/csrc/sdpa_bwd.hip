@@ -829,7 +829,7 @@ void sdpa_bwd_dkdv_f32_kernel(const BwdParams p) {
 // ---------------------------------------------------------------------------
 // Host launcher: dQ (+ delta) first, then dK/dV, on the caller's stream.
 // ---------------------------------------------------------------------------
-hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, hipStream_t stream) {
+hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, int phases, hipStream_t stream) {
     const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv;
     if (B == 0) return hipSuccess;
     const bool drop = p.c.use_dropout != 0;
@@ -839,24 +839,27 @@ hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, hipStream_t str
                 return with_bool(drop, [&](auto d) {
                     constexpr int DQK = decltype(dqk)::value, DV = decltype(dv)::value;
                     constexpr bool V = decltype(v)::value, D = decltype(d)::value;
-                    hipError_t err;
+                    hipError_t err = hipSuccess;
                     if (dtype == DType::F16) {
                         using CQ = BwdQF16Cfg<DQK, DV>;
                         using CK = BwdKVF16Cfg<DQK, DV>;
                         const unsigned gq = (unsigned)(((S_q + CQ::BM - 1) / CQ::BM) * B);
                         const unsigned gk = (unsigned)(((S_kv + CK::BKV - 1) / CK::BKV) * B);
-                        err = launch_kernel<sdpa_bwd_dq_f16_kernel<DQK, DV, V, D>>(gq, CQ::NT, CQ::LDS_BYTES, stream, p);
-                        if (err != hipSuccess) return err;
-                        return launch_kernel<sdpa_bwd_dkdv_f16_kernel<DQK, DV, V, D>>(gk, CK::NT, CK::LDS_BYTES, stream, p);
+                        if (phases & kBwdDq)
+                            err = launch_kernel<sdpa_bwd_dq_f16_kernel<DQK, DV, V, D>>(gq, CQ::NT, CQ::LDS_BYTES, stream, p);
+                        if (err == hipSuccess && (phases & kBwdDkDv))
+                            err = launch_kernel<sdpa_bwd_dkdv_f16_kernel<DQK, DV, V, D>>(gk, CK::NT, CK::LDS_BYTES, stream, p);
                     } else {
                         using CQ = BwdQF32Cfg<DQK, DV>;
                         using CK = BwdKVF32Cfg<DQK, DV>;
                         const unsigned gq = (unsigned)(((S_q + CQ::BM - 1) / CQ::BM) * B);
                         const unsigned gk = (unsigned)(((S_kv + CK::BKV - 1) / CK::BKV) * B);
-                        err = launch_kernel<sdpa_bwd_dq_f32_kernel<DQK, DV, V, D>>(gq, CQ::NT, CQ::LDS_BYTES, stream, p);
-                        if (err != hipSuccess) return err;
-                        return launch_kernel<sdpa_bwd_dkdv_f32_kernel<DQK, DV, V, D>>(gk, CK::NT, CK::LDS_BYTES, stream, p);
+                        if (phases & kBwdDq)
+                            err = launch_kernel<sdpa_bwd_dq_f32_kernel<DQK, DV, V, D>>(gq, CQ::NT, CQ::LDS_BYTES, stream, p);
+                        if (err == hipSuccess && (phases & kBwdDkDv))
+                            err = launch_kernel<sdpa_bwd_dkdv_f32_kernel<DQK, DV, V, D>>(gk, CK::NT, CK::LDS_BYTES, stream, p);
                     }
+                    return err;
                 });
             });
         });

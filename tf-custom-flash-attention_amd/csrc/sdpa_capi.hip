@@ -185,19 +185,25 @@ size_t sdpa_hip_bwd_workspace_bytes(int B, int S_q) {
     return (bytes + 255) & ~(size_t)255;
 }
 
-int sdpa_hip_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
-                 const float* stats, const void* d_o, void* dq, void* dk, void* dv,
-                 void* workspace, size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk,
-                 int D_v, float scale, float dropout, int causal_mask, uint64_t seed,
-                 uint64_t offset, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+// Shared body of the three backward entry points.
+int bwd_entry(int phases, int dtype, const void* q, const void* k, const void* v, const void* o,
+              const float* stats, const void* d_o, void* dq, void* dk, void* dv, void* workspace,
+              size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v, float scale,
+              float dropout, int causal_mask, uint64_t seed, uint64_t offset, hipStream_t stream) {
     int st = check_common(dtype, B, S_q, S_kv, D_qk, D_v, dropout, causal_mask);
     if (st != SDPA_OK) return st;
     if (B == 0) return SDPA_OK;
     if (workspace_bytes < sdpa_hip_bwd_workspace_bytes(B, S_q)) return SDPA_ERR_WORKSPACE;
     const bool has_q = (size_t)S_q > 0, has_kv = (size_t)S_kv > 0;
-    if ((has_q && (!stats || !workspace)) || (has_q && D_qk > 0 && (!q || !dq)) ||
-        (has_q && D_v > 0 && (!o || !d_o)) || (has_kv && D_qk > 0 && (!k || !dk)) ||
-        (has_kv && D_v > 0 && (!v || !dv)))
+    const bool want_dq = phases & sdpa::kBwdDq, want_kv = phases & sdpa::kBwdDkDv;
+    if ((has_q && (!stats || !workspace)) || (has_q && D_qk > 0 && !q) ||
+        (has_q && D_v > 0 && !d_o) || (want_dq && has_q && D_qk > 0 && !dq) ||
+        (want_dq && has_q && D_v > 0 && !o) || (has_kv && D_qk > 0 && !k) ||
+        (has_kv && D_v > 0 && !v) || (want_kv && has_kv && D_qk > 0 && !dk) ||
+        (want_kv && has_kv && D_v > 0 && !dv))
         return SDPA_ERR_NULL_POINTER;
     sdpa::BwdParams p{};
     p.q = q;
@@ -212,8 +218,43 @@ int sdpa_hip_bwd(int dtype, const void* q, const void* k, const void* v, const v
     p.delta = static_cast<float*>(workspace);
     p.s = sdpa::AttnShape{B, S_q, S_kv, D_qk, D_v};
     p.c = make_scalars(scale, dropout, causal_mask, seed, offset);
-    const bool vec = vec_ok(dtype, D_qk, D_v, {q, k, v, o, d_o, dq, dk, dv});
-    return hip_status(sdpa::launch_bwd(p, (sdpa::DType)dtype, vec, stream));
+    const bool vec = vec_ok(dtype, D_qk, D_v,
+                            {q, k, v, d_o, want_dq ? o : nullptr, want_dq ? dq : nullptr,
+                             want_kv ? dk : nullptr, want_kv ? dv : nullptr});
+    return hip_status(sdpa::launch_bwd(p, (sdpa::DType)dtype, vec, phases, stream));
+}
+}  // namespace
+
+extern "C" {
+
+int sdpa_hip_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
+                 const float* stats, const void* d_o, void* dq, void* dk, void* dv,
+                 void* workspace, size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk,
+                 int D_v, float scale, float dropout, int causal_mask, uint64_t seed,
+                 uint64_t offset, hipStream_t stream) {
+    return bwd_entry(sdpa::kBwdDq | sdpa::kBwdDkDv, dtype, q, k, v, o, stats, d_o, dq, dk, dv,
+                     workspace, workspace_bytes, B, S_q, S_kv, D_qk, D_v, scale, dropout,
+                     causal_mask, seed, offset, stream);
+}
+
+int sdpa_hip_bwd_dq(int dtype, const void* q, const void* k, const void* v, const void* o,
+                    const float* stats, const void* d_o, void* dq, void* workspace,
+                    size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
+                    float scale, float dropout, int causal_mask, uint64_t seed, uint64_t offset,
+                    hipStream_t stream) {
+    return bwd_entry(sdpa::kBwdDq, dtype, q, k, v, o, stats, d_o, dq, nullptr, nullptr, workspace,
+                     workspace_bytes, B, S_q, S_kv, D_qk, D_v, scale, dropout, causal_mask, seed,
+                     offset, stream);
+}
+
+int sdpa_hip_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, const float* stats,
+                      const void* d_o, void* dk, void* dv, const void* workspace,
+                      size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
+                      float scale, float dropout, int causal_mask, uint64_t seed,
+                      uint64_t offset, hipStream_t stream) {
+    return bwd_entry(sdpa::kBwdDkDv, dtype, q, k, v, nullptr, stats, d_o, nullptr, dk, dv,
+                     const_cast<void*>(workspace), workspace_bytes, B, S_q, S_kv, D_qk, D_v, scale,
+                     dropout, causal_mask, seed, offset, stream);
 }
 
 uint64_t sdpa_hip_drop_threshold(float dropout) { return drop_threshold_impl(dropout); }

@@ -51,6 +51,8 @@ hipError_t launch_kernel(unsigned grid, unsigned block, size_t lds, hipStream_t 
 }
 
 hipError_t launch_fwd(const FwdParams& p, DType dtype, bool vec, hipStream_t stream);
-hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, hipStream_t stream);
+// phases: kBwdDq (dQ kernel, writes delta) and/or kBwdDkDv (reads delta).
+constexpr int kBwdDq = 1, kBwdDkDv = 2;
+hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, int phases, hipStream_t stream);
 
 }  // namespace sdpa
