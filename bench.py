@@ -221,8 +221,10 @@ def main():
     kflops = {"sdpa_fwd": f_fwd, "sdpa_bwd_dq": f_dq, "sdpa_bwd_dkdv": f_dkdv}
     dom = max(per, key=per.get)
     achieved = kflops[dom] / (per[dom] * 1e-3) / 1e12
-    kernel_symbol = {"sdpa_fwd": "sdpa_fwd_%s_kernel" % dt, "sdpa_bwd_dq": "sdpa_bwd_dq_%s_kernel" % dt,
-                     "sdpa_bwd_dkdv": "sdpa_bwd_dkdv_%s_kernel" % dt}[dom]
+    # fp16 shapes with D % 8 == 0 run the DMA-fed kernels (sdpa_f16_dma.hip)
+    sfx = "f16_dma" if (dt == "f16" and D_qk % 8 == 0 and D_v % 8 == 0) else dt
+    kernel_symbol = {"sdpa_fwd": "sdpa_fwd_%s_kernel" % sfx, "sdpa_bwd_dq": "sdpa_bwd_dq_%s_kernel" % sfx,
+                     "sdpa_bwd_dkdv": "sdpa_bwd_dkdv_%s_kernel" % sfx}[dom]
 
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * (1 << 20)

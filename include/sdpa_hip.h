@@ -100,8 +100,8 @@ int sdpa_hip_fwd(int dtype, const void* q, const void* k, const void* v, void* o
 
 /* ---- backward: replaces FlashAttnGradFunctor<GPUDevice,T> (sdpa/sdpa_bwd.cu.cc:347-453)
  * Needs a device workspace of sdpa_hip_bwd_workspace_bytes(B, S_q) bytes
- * (the per-row delta = sum_d dO * O, fp32), provided by the caller as the
- * TF op does with allocate_temp.                                             */
+ * (two fp32 values per query row: stats * log2(e) and delta = sum_d dO * O),
+ * provided by the caller as the TF op does with allocate_temp.              */
 size_t sdpa_hip_bwd_workspace_bytes(int B, int S_q);
 
 int sdpa_hip_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
@@ -113,8 +113,8 @@ int sdpa_hip_bwd(int dtype, const void* q, const void* k, const void* v, const v
 /* The two launches of sdpa_hip_bwd as separate calls, same arguments, same
  * stream order required (the reference launches its two backward kernels
  * back to back, sdpa/sdpa_bwd.cu.cc:402-405):
- *   sdpa_hip_bwd_dq   -- dQ, and delta into the workspace;
- *   sdpa_hip_bwd_dkdv -- dK and dV, reading the delta left in the workspace
+ *   sdpa_hip_bwd_dq   -- dQ, and the per-row values into the workspace;
+ *   sdpa_hip_bwd_dkdv -- dK and dV, reading the values left in the workspace
  *                        by a preceding sdpa_hip_bwd_dq with the same inputs.
  * sdpa_hip_bwd == sdpa_hip_bwd_dq followed by sdpa_hip_bwd_dkdv.            */
 int sdpa_hip_bwd_dq(int dtype, const void* q, const void* k, const void* v, const void* o,

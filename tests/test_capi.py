@@ -153,7 +153,8 @@ def test_launch_entry_points_reject_before_device_work(pkg):
                                           null, ws_bytes, 2, 4, 4, 8, 8, 1.0, 0.0, 0, 0, 0, null)
     assert bwd(0) == 22                                  # workspace too small
     assert L.sdpa_hip_bwd_workspace_bytes(2, 4) == 256
-    assert L.sdpa_hip_bwd_workspace_bytes(128, 4096) == 128 * 4096 * 4
+    # two fp32 rows per query row: stats * log2(e) and delta
+    assert L.sdpa_hip_bwd_workspace_bytes(128, 4096) == 2 * 128 * 4096 * 4
     assert L.sdpa_hip_bwd_workspace_bytes(0, 4096) == 0
 
 

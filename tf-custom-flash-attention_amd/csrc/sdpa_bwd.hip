@@ -93,9 +93,12 @@ void sdpa_bwd_dq_f16_kernel(const BwdParams p) {
     }
     const float delta = xhalf_sum(dpart);
     const bool row_ok = my_q < S_q;
-    if (row_ok && hh == 0) p.delta[row_q] = delta;
     // P = exp2(fma(s, scale*log2e, -stats*log2e)); rows past S_q get P = 0.
     const float stats2 = row_ok ? p.stats[row_q] * kLog2e : INFINITY;
+    if (row_ok && hh == 0) {
+        p.delta[row_q] = delta;
+        p.stats2[row_q] = stats2;
+    }
     const float sl2 = p.c.scale_log2;
     const float ksc = p.c.keep_scale;
 
@@ -521,8 +524,11 @@ void sdpa_bwd_dq_f32_kernel(const BwdParams p) {
     }
     const float delta = xhalf_sum(dpart);
     const bool row_ok = my_q < S_q;
-    if (row_ok && hh == 0) p.delta[row_q] = delta;
     const float stats2 = row_ok ? p.stats[row_q] * kLog2e : INFINITY;
+    if (row_ok && hh == 0) {
+        p.delta[row_q] = delta;
+        p.stats2[row_q] = stats2;
+    }
     const float sl2 = p.c.scale_log2;
     const float ksc = p.c.keep_scale;
 

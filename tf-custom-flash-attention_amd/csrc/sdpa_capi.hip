@@ -176,12 +176,14 @@ int sdpa_hip_fwd(int dtype, const void* q, const void* k, const void* v, void* o
     p.s = sdpa::AttnShape{B, S_q, S_kv, D_qk, D_v};
     p.c = make_scalars(scale, dropout, causal_mask, seed, offset);
     const bool vec = vec_ok(dtype, D_qk, D_v, {q, k, v, o});
+    if (dtype == SDPA_DTYPE_F16 && vec) return hip_status(sdpa::launch_fwd_f16_dma(p, stream));
     return hip_status(sdpa::launch_fwd(p, (sdpa::DType)dtype, vec, stream));
 }
 
 size_t sdpa_hip_bwd_workspace_bytes(int B, int S_q) {
     if (B <= 0 || S_q <= 0) return 0;
-    const size_t bytes = (size_t)B * (size_t)S_q * sizeof(float);
+    // stats * log2(e) and delta, one fp32 row each per query row.
+    const size_t bytes = 2 * (size_t)B * (size_t)S_q * sizeof(float);
     return (bytes + 255) & ~(size_t)255;
 }
 
@@ -215,12 +217,14 @@ int bwd_entry(int phases, int dtype, const void* q, const void* k, const void* v
     p.dq = dq;
     p.dk = dk;
     p.dv = dv;
-    p.delta = static_cast<float*>(workspace);
+    p.stats2 = static_cast<float*>(workspace);
+    p.delta = static_cast<float*>(workspace) + (size_t)B * S_q;
     p.s = sdpa::AttnShape{B, S_q, S_kv, D_qk, D_v};
     p.c = make_scalars(scale, dropout, causal_mask, seed, offset);
     const bool vec = vec_ok(dtype, D_qk, D_v,
                             {q, k, v, d_o, want_dq ? o : nullptr, want_dq ? dq : nullptr,
                              want_kv ? dk : nullptr, want_kv ? dv : nullptr});
+    if (dtype == SDPA_DTYPE_F16 && vec) return hip_status(sdpa::launch_bwd_f16_dma(p, phases, stream));
     return hip_status(sdpa::launch_bwd(p, (sdpa::DType)dtype, vec, phases, stream));
 }
 }  // namespace

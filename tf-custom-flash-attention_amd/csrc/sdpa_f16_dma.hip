@@ -1,0 +1,740 @@
+// sdpa_f16_dma.hip -- fp16 Sdpa / SdpaGrad kernels for gfx950 that stream
+// their K/V (forward, dQ) or Q/dO (dK/dV) tiles from HBM straight into LDS.
+//
+// These are the production kernels for the fp16 op whenever every feature
+// width is a multiple of 8 and every tensor is 16-byte aligned (the shapes
+// the reference's MHA layer produces, sdpa_fwd.cu.cc:191-215 dispatch up to
+// D = 128).  Other fp16 shapes use the register-staged kernels of
+// sdpa_fwd.hip / sdpa_bwd.hip, which accept any D.
+//
+// Data movement.  Tiles are copied by buffer_load_dwordx4 ... lds: lane L of
+// a wave writes 16 bytes to LDS at (wave base + 16 L), and each lane picks
+// the global chunk that belongs there, so the LDS image comes out in the
+// chunk-swizzled layout of swz_off() (conflict-free row and transpose reads)
+// without passing through VGPRs.  The buffer descriptor of every tile starts
+// at the tile's first row and ends at the end of the batch row, so rows past
+// S and columns past D read as zero: tails need no branches.  Two LDS stages:
+// the copy of step n+1 is in flight while step n is multiplied, with one
+// barrier per step.
+//
+// Work order.  Workgroup ids are remapped so that each XCD (ids are dealt
+// round-robin over the 8 XCDs) walks whole batch rows: all tiles of a batch
+// row run on one XCD and share its L2 copy of the streamed operands.  Under
+// causal masking the heaviest tiles of a batch row go first.
+//
+// MFMA formulation (v_mfma_f32_32x32x16_f16, fp32 accumulation; the lane
+// layouts are listed in sdpa_device.h):
+//   forward, per wave of 32 queries (lane = query):
+//     S^T = K Q^T, online softmax over keys, O^T += V^T P~^T
+//   dQ, per wave of 32 queries:
+//     S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T
+//   dK/dV, per wave of 32 keys (lane = key):
+//     S = Q K^T, dP = dO V^T, dV^T += dO^T P~, dK^T += Q^T dS
+// Element semantics are those of the reference (sdpa/sdpa_fwd.cu.cc:93-173,
+// sdpa/sdpa_bwd.cu.cc:130-170, 291-327), restated in sdpa_fwd.hip and
+// sdpa_bwd.hip.
+#include "sdpa_device.h"
+#include "sdpa_launch.h"
+#include "sdpa_params.h"
+#include "sdpa_tile.h"
+
+namespace sdpa {
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// A voffset at or past num_records: the load returns zero and touches nothing.
+constexpr uint32_t kOob = 0x80000000u;
+// Lazy-rescale threshold of the forward's running maximum (log2 units).
+constexpr float kTauF = 8.0f;
+
+// Raw buffer descriptor over [base, base + bytes).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, long long bytes) {
+    const int n = bytes <= 0 ? 0 : (bytes >= 0x7FFFFFFFLL ? 0x7FFFFFFF : (int)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+// 16 (or 4) bytes per lane from byte offset voff into LDS at wave_dst + 16 L (4 L).
+__device__ __forceinline__ void dma16(rsrc_t r, unsigned char* wave_dst, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)wave_dst, 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void dma4(rsrc_t r, unsigned char* wave_dst, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)wave_dst, 4, voff, 0, 0, 0);
+}
+// s_waitcnt vmcnt(0): this wave's copies (and loads) have landed.
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Per-lane global offsets of one ROWS x (8 L) fp16 tile copied by 4 waves.
+// LDS chunk slot p (16 bytes) of the tile is row p / L, position p % L; it
+// receives global chunk (p % L) ^ swz<L>(row) of that row.  Copy u of wave w
+// fills slots (4 u + w) * 64 + lane, i.e. rows (4 u + w) * 64 / L + lane / L;
+// for every L the swizzle term of those rows does not depend on u, so one
+// offset per lane plus u * (256 / L) rows covers all of the wave's copies.
+template <int ROWS, int L>
+struct TileDma {
+    static constexpr int LOADS = ROWS * L / 64;  // wave-sized copies per tile
+    static constexpr int PER_WAVE = LOADS / 4;
+    static_assert(LOADS % 4 == 0, "a tile is split evenly over the 4 waves");
+    uint32_t voff0;     // offset of copy 0, or kOob for chunks past D
+    uint32_t row_step;  // bytes between consecutive copies of a wave
+
+    // row_bytes: global row pitch; valid_chunks: 16-byte chunks inside D.
+    __device__ __forceinline__ void init(int wave, int lane, int row_bytes, int valid_chunks) {
+        const int slot = wave * 64 + lane;
+        const int r = slot / L;
+        const int c = (slot % L) ^ swz<L>(r);
+        voff0 = c < valid_chunks ? (uint32_t)(r * row_bytes + c * 16) : kOob;
+        row_step = (uint32_t)((256 / L) * row_bytes);
+    }
+    __device__ __forceinline__ void issue(rsrc_t rs, unsigned char* tile, int wave) const {
+#pragma unroll
+        for (int u = 0; u < PER_WAVE; ++u) dma16(rs, tile + (u * 4 + wave) * 1024, voff0 + u * row_step);
+    }
+};
+
+// Workgroup id -> (batch, tile), XCD-major: XCD x (ids x, x+8, ...) owns a
+// contiguous range of the batch-major tile list.  `reverse` issues the tiles
+// of a batch row last-first.
+__device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles, bool reverse, int& b, int& t) {
+    const int xcd = bid & 7, local = bid >> 3;
+    const int per = nblocks >> 3, rem = nblocks & 7;
+    const int lin = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+    b = lin / tiles;
+    const int r = lin - b * tiles;
+    t = reverse ? tiles - 1 - r : r;
+}
+
+// Two fp32 values -> one dword of two RNE-rounded halves (v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, half2v));
+}
+
+__device__ __forceinline__ half8 half8_of(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(half8, (u4){w0, w1, w2, w3});
+}
+
+// Per-lane LDS byte offsets of the MFMA A-operand reads from a swizzled
+// fp16 tile with L 16-byte chunks per row (see swz_off).  The swizzle only
+// permutes chunks inside a 16 L-byte row and every tile base is a multiple of
+// 256 bytes, so each read is (tile base + lane term) ^ constant, with the
+// tile's row offset in the instruction's immediate field:
+//   row read,  rows R0 + l32 (R0 % 16 == 0), features 16 ks + 8 hh .. +7:
+//              ((base + row) ^ (32 ks)) + 16 L R0
+//   transposed read of rows R0 + 16 s + {tr_row, tr_row + 8} (see
+//   lds_read_tr), features 32 dt + tr_col:
+//              ((base + tr[j]) ^ (64 dt)) + 16 L (R0 + 16 s)
+template <int L>
+struct SwzLane {
+    uint32_t row, tr0, tr1;
+    __device__ __forceinline__ void init(int lane) {
+        const int l32 = lane & 31, hh = lane >> 5;
+        row = (uint32_t)(l32 * 16 * L + 16 * (hh ^ swz<L>(l32)));
+        const int g16 = lane >> 4, i16 = lane & 15;
+        const int tr_row = 4 * (g16 >> 1) + (i16 >> 2);
+        const int c = 2 * (g16 & 1) + ((i16 & 3) >> 1);  // chunk of column tr_col within 32 features
+        const int sub = 8 * (i16 & 1);                   // byte of column tr_col within its chunk
+        tr0 = (uint32_t)(tr_row * 16 * L + 16 * (c ^ swz<L>(tr_row)) + sub);
+        tr1 = (uint32_t)((tr_row + 8) * 16 * L + 16 * (c ^ swz<L>(tr_row + 8)) + sub);
+    }
+};
+
+extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+
+// Row-read A operand: rows R0 + l32 (R0 % 16 == 0), k-step ks.
+// `a` = tile base + SwzLane::row.
+template <int L>
+__device__ __forceinline__ half8 lds_row(uint32_t a, int ks, int R0) {
+    return *reinterpret_cast<const half8*>(smem + ((a ^ (uint32_t)(32 * ks)) + 16 * L * R0));
+}
+
+// Transposed A operand: tile rows R0 .. R0 + 15 (R0 % 16 == 0) in the order
+// of the accumulator layout, features 32 dt + (0..31).
+// a0 / a1 = tile base + SwzLane::tr0 / tr1.
+template <int L>
+__device__ __forceinline__ half8 lds_tr(uint32_t a0, uint32_t a1, int dt, int R0) {
+    const half4 x0 = lds_read_tr(reinterpret_cast<const half_t*>(smem + ((a0 ^ (uint32_t)(64 * dt)) + 16 * L * R0)));
+    const half4 x1 = lds_read_tr(reinterpret_cast<const half_t*>(smem + ((a1 ^ (uint32_t)(64 * dt)) + 16 * L * R0)));
+    return __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Store 16 fp32 accumulator rows of a C^T tile (lane = output row, in-lane =
+// features 32 dt + 8 g + 4 hh + e) as fp16 with a common factor.
+template <int DN>
+__device__ __forceinline__ void store_rows_f16(half_t* dst, const floatx16 (&acc)[DN / 32], float f, int hh) {
+#pragma unroll
+    for (int dt = 0; dt < DN / 32; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            half4 hv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hv[e] = (half_t)(acc[dt][4 * g + e] * f);
+            *reinterpret_cast<half4*>(dst + 32 * dt + 8 * g + 4 * hh) = hv;
+        }
+}
+
+// Same, columns >= ncols not written (D < padded width).
+template <int DN>
+__device__ __forceinline__ void store_rows_f16_n(half_t* dst, const floatx16 (&acc)[DN / 32], float f, int hh,
+                                                 int ncols) {
+#pragma unroll
+    for (int dt = 0; dt < DN / 32; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 32 * dt + 8 * g + 4 * hh;
+            if (d0 < ncols) {
+                half4 hv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) hv[e] = (half_t)(acc[dt][4 * g + e] * f);
+                *reinterpret_cast<half4*>(dst + d0) = hv;
+            }
+        }
+}
+
+// ===========================================================================
+// Forward
+// ===========================================================================
+template <int DQK, int DV>
+struct FwdDmaCfg {
+    static constexpr int NT = 256, BM = 128, BN = 64;
+    static constexpr int LK = DQK / 8, LV = DV / 8;
+    static constexpr int KB = BN * DQK * 2, VB = BN * DV * 2, STAGE = KB + VB;
+    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+};
+
+template <int DQK, int DV, bool CAUSAL, bool DROP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
+    using Cfg = FwdDmaCfg<DQK, DV>;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV;
+
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
+    const int tiles = (S_q + BM - 1) / BM;
+    int b, qt;
+    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, b, qt);
+    const int q0 = qt * BM, qw0 = q0 + 32 * wave, my_q = qw0 + l32;
+
+    const half_t* Qb = static_cast<const half_t*>(p.q) + (size_t)b * S_q * D_qk;
+    const half_t* Kb = static_cast<const half_t*>(p.k) + (size_t)b * S_kv * D_qk;
+    const half_t* Vb = static_cast<const half_t*>(p.v) + (size_t)b * S_kv * D_v;
+
+    // The running maximum is taken on raw scores q.k, which needs a
+    // non-negative factor: for scale < 0 the queries are negated in
+    // registers (exact) and |scale| used.  A zero factor is replaced by
+    // 1e-30, which leaves every probability 1 to within 1e-26.
+    const float sl2_raw = p.c.scale_log2;
+    const bool neg = sl2_raw < 0.f;
+    const float sl2 = (sl2_raw == 0.f) ? 1e-30f : fabsf(sl2_raw);
+
+    half8 qreg[DQK / 16];
+#pragma unroll
+    for (int ks = 0; ks < DQK / 16; ++ks) {
+        half8 v = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Qb, my_q, S_q, 16 * ks + 8 * hh, D_qk, D_qk));
+        qreg[ks] = neg ? -v : v;
+    }
+
+    TileDma<BN, LK> kd;
+    TileDma<BN, LV> vd;
+    kd.init(wave, lane, D_qk * 2, D_qk / 8);
+    vd.init(wave, lane, D_v * 2, D_v / 8);
+    const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
+    const int nsteps = (kv_end + BN - 1) / BN;
+    auto issue = [&](int step) {
+        const int kv0 = step * BN;
+        unsigned char* st = smem + (step & 1) * Cfg::STAGE;
+        kd.issue(make_rsrc(Kb + (size_t)kv0 * D_qk, (long long)(S_kv - kv0) * D_qk * 2), st, wave);
+        vd.issue(make_rsrc(Vb + (size_t)kv0 * D_v, (long long)(S_kv - kv0) * D_v * 2), st + Cfg::KB, wave);
+    };
+    if (nsteps > 0) issue(0);
+
+    floatx16 oacc[DV / 32];
+#pragma unroll
+    for (int dt = 0; dt < DV / 32; ++dt) oacc[dt] = floatx16{};
+    float m_run = kMaxSentinel, l_run = 0.f;
+
+    // Dropout hash of (my_q, key 4 hh); element (key kv0 + c) adds (kv0 + c) A.
+    const uint64_t st_lane = DROP ? lcg_state(p.c.seed_offset, (uint64_t)b * S_q + my_q, (uint64_t)S_kv, 4 * hh) : 0;
+    const uint32_t thr = p.c.drop_threshold;
+
+    SwzLane<LK> swK;
+    SwzLane<LV> swV;
+    swK.init(lane);
+    swV.init(lane);
+
+    for (int step = 0; step < nsteps; ++step) {
+        wait_vm();
+        __syncthreads();
+        if (step + 1 < nsteps) issue(step + 1);
+        if (qw0 >= S_q) continue;
+        const int kv0 = step * BN;
+        const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE), vbase = kbase + Cfg::KB;
+        const uint32_t aK = kbase + swK.row, aV0 = vbase + swV.tr0, aV1 = vbase + swV.tr1;
+
+        // 32-key sub-tiles: live (any visible key) and part (needs masking).
+        bool live[2], part[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int k0 = kv0 + 32 * t;
+            live[t] = k0 < S_kv && (!CAUSAL || k0 <= qw0 + 31);
+            part[t] = k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0);
+        }
+
+        // ---- S^T = K Q^T ------------------------------------------------
+        floatx16 s[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            s[t] = floatx16{};
+            if (live[t]) {
+#pragma unroll
+                for (int ks = 0; ks < DQK / 16; ++ks)
+                    s[t] = mfma_f16(lds_row<LK>(aK, ks, 32 * t), qreg[ks], s[t]);
+                if (part[t]) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * hh + (r & 3);
+                        if (key >= S_kv || (CAUSAL && key > my_q)) s[t][r] = -INFINITY;
+                    }
+                }
+            }
+        }
+
+        // ---- running maximum (raw scores), lazy rescale --------------------
+        float mx = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            if (live[t])
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[t][r], s[t][r + 1]));
+        mx = xhalf_max(mx) * sl2;
+        if (wave_any(mx > m_run + kTauF)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = fast_exp2(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+            m_run = m_new;
+        }
+
+        // ---- P = exp2(s*sl2 - m), undropped sum, dropout, fp16 B operands ---
+        const float nm = -m_run;
+        const uint64_t st_blk = DROP ? st_lane + (uint64_t)kv0 * kLcgMul : 0;
+        half8 pb[4];
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (!live[t]) continue;
+            uint32_t w[8];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                float p0 = fast_exp2(__builtin_fmaf(s[t][r], sl2, nm));
+                float p1 = fast_exp2(__builtin_fmaf(s[t][r + 1], sl2, nm));
+                ls[(r >> 2) & 3] += p0 + p1;
+                if constexpr (DROP) {
+                    const int c0 = 32 * t + 8 * (r >> 2) + (r & 3);
+                    p0 = lcg_keep(st_blk + (uint64_t)c0 * kLcgMul, thr) ? p0 : 0.f;
+                    p1 = lcg_keep(st_blk + (uint64_t)(c0 + 1) * kLcgMul, thr) ? p1 : 0.f;
+                }
+                w[r >> 1] = pack_h2(p0, p1);
+            }
+            pb[2 * t] = half8_of(w[0], w[1], w[2], w[3]);
+            pb[2 * t + 1] = half8_of(w[4], w[5], w[6], w[7]);
+        }
+        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+
+        // ---- O^T += V^T P~^T ----------------------------------------------
+#pragma unroll
+        for (int sk = 0; sk < 4; ++sk) {
+            if (!live[sk >> 1]) continue;
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt)
+                oacc[dt] = mfma_f16(lds_tr<LV>(aV0, aV1, dt, 16 * sk), pb[sk], oacc[dt]);
+        }
+    }
+
+    // ---- epilogue: stats = m + log(l + 1e-6), O = acc / l (0 if l <= 1e-6) ----
+    const float l_tot = xhalf_sum(l_run);
+    if (my_q < S_q) {
+        const float m_nat = (l_tot > 0.f) ? m_run * kLn2 : kNegInf;
+        if (hh == 0) p.stats[(size_t)b * S_q + my_q] = m_nat + logf(l_tot + kEps);
+        const float inv = (l_tot > kEps) ? p.c.keep_scale / l_tot : 0.f;
+        half_t* Ob = static_cast<half_t*>(p.o) + ((size_t)b * S_q + my_q) * D_v;
+        if (D_v == DV) store_rows_f16<DV>(Ob, oacc, inv, hh);
+        else store_rows_f16_n<DV>(Ob, oacc, inv, hh, D_v);
+    }
+}
+
+// ===========================================================================
+// Backward, dQ kernel (also writes stats2 and delta to the workspace)
+// ===========================================================================
+template <int DQK, int DV>
+struct DqDmaCfg {
+    static constexpr int NT = 256, BM = 128, BN = 64;
+    static constexpr int LK = DQK / 8, LV = DV / 8;
+    static constexpr int KB = BN * DQK * 2, VB = BN * DV * 2, STAGE = KB + VB;
+    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+};
+
+template <int DQK, int DV, bool CAUSAL, bool DROP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
+    using Cfg = DqDmaCfg<DQK, DV>;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV;
+
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
+    const int tiles = (S_q + BM - 1) / BM;
+    int b, qt;
+    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, b, qt);
+    const int q0 = qt * BM, qw0 = q0 + 32 * wave, my_q = qw0 + l32;
+    const size_t row_q = (size_t)b * S_q + my_q;
+
+    const half_t* Qb = static_cast<const half_t*>(p.q) + (size_t)b * S_q * D_qk;
+    const half_t* Ob = static_cast<const half_t*>(p.o) + (size_t)b * S_q * D_v;
+    const half_t* dOb = static_cast<const half_t*>(p.d_o) + (size_t)b * S_q * D_v;
+    const half_t* Kb = static_cast<const half_t*>(p.k) + (size_t)b * S_kv * D_qk;
+    const half_t* Vb = static_cast<const half_t*>(p.v) + (size_t)b * S_kv * D_v;
+
+    half8 qreg[DQK / 16], doreg[DV / 16];
+#pragma unroll
+    for (int ks = 0; ks < DQK / 16; ++ks)
+        qreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Qb, my_q, S_q, 16 * ks + 8 * hh, D_qk, D_qk));
+    float dpart = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < DV / 16; ++ks) {
+        doreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(dOb, my_q, S_q, 16 * ks + 8 * hh, D_v, D_v));
+        const half8 o8 = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Ob, my_q, S_q, 16 * ks + 8 * hh, D_v, D_v));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dpart += (float)doreg[ks][e] * (float)o8[e];
+    }
+    const float delta = xhalf_sum(dpart);
+    const bool row_ok = my_q < S_q;
+    const float stats2 = row_ok ? p.stats[row_q] * kLog2e : INFINITY;
+    if (row_ok && hh == 0) {
+        p.delta[row_q] = delta;
+        p.stats2[row_q] = stats2;
+    }
+    const float sl2 = p.c.scale_log2;
+    const float ksc = p.c.keep_scale;
+    const float nst = -stats2;
+
+    TileDma<BN, LK> kd;
+    TileDma<BN, LV> vd;
+    kd.init(wave, lane, D_qk * 2, D_qk / 8);
+    vd.init(wave, lane, D_v * 2, D_v / 8);
+    const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
+    const int nsteps = (kv_end + BN - 1) / BN;
+    auto issue = [&](int step) {
+        const int kv0 = step * BN;
+        unsigned char* st = smem + (step & 1) * Cfg::STAGE;
+        kd.issue(make_rsrc(Kb + (size_t)kv0 * D_qk, (long long)(S_kv - kv0) * D_qk * 2), st, wave);
+        vd.issue(make_rsrc(Vb + (size_t)kv0 * D_v, (long long)(S_kv - kv0) * D_v * 2), st + Cfg::KB, wave);
+    };
+    if (nsteps > 0) issue(0);
+
+    const uint64_t st_lane = DROP ? lcg_state(p.c.seed_offset, row_q, (uint64_t)S_kv, 4 * hh) : 0;
+    const uint32_t thr = p.c.drop_threshold;
+
+    SwzLane<LK> swK;
+    SwzLane<LV> swV;
+    swK.init(lane);
+    swV.init(lane);
+
+    floatx16 dqacc[DQK / 32];
+#pragma unroll
+    for (int dt = 0; dt < DQK / 32; ++dt) dqacc[dt] = floatx16{};
+
+    for (int step = 0; step < nsteps; ++step) {
+        wait_vm();
+        __syncthreads();
+        if (step + 1 < nsteps) issue(step + 1);
+        if (qw0 >= S_q) continue;
+        const int kv0 = step * BN;
+        const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE), vbase = kbase + Cfg::KB;
+        const uint32_t aK = kbase + swK.row, aV = vbase + swV.row;
+        const uint32_t aK0 = kbase + swK.tr0, aK1 = kbase + swK.tr1;
+
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int k0 = kv0 + 32 * t;
+            if (!(k0 < S_kv && (!CAUSAL || k0 <= qw0 + 31))) continue;
+            const bool part = k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0);
+
+            floatx16 sacc = floatx16{}, dpacc = floatx16{};
+#pragma unroll
+            for (int ks = 0; ks < DQK / 16; ++ks)
+                sacc = mfma_f16(lds_row<LK>(aK, ks, 32 * t), qreg[ks], sacc);
+#pragma unroll
+            for (int ks = 0; ks < DV / 16; ++ks)
+                dpacc = mfma_f16(lds_row<LV>(aV, ks, 32 * t), doreg[ks], dpacc);
+
+            // rows of the accumulators are keys k0 + 8 (r/4) + 4 hh + r%4
+            const uint64_t st_blk = DROP ? st_lane + (uint64_t)k0 * kLcgMul : 0;
+            uint32_t w[8];
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                float ds2[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int rr = r + e;
+                    float x = __builtin_fmaf(sacc[rr], sl2, nst);
+                    if (part) {
+                        const int key = k0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
+                        if (key >= S_kv || (CAUSAL && key > my_q)) x = -INFINITY;
+                    }
+                    const float pr = fast_exp2(x);
+                    float tt;
+                    if constexpr (DROP) {
+                        const bool keep = lcg_keep(st_blk + (uint64_t)(8 * (rr >> 2) + (rr & 3)) * kLcgMul, thr);
+                        tt = keep ? __builtin_fmaf(dpacc[rr], ksc, -delta) : -delta;
+                    } else {
+                        tt = dpacc[rr] - delta;
+                    }
+                    ds2[e] = pr > kEps ? pr * tt : 0.f;
+                }
+                w[r >> 1] = pack_h2(ds2[0], ds2[1]);
+            }
+            const half8 dsb0 = half8_of(w[0], w[1], w[2], w[3]);
+            const half8 dsb1 = half8_of(w[4], w[5], w[6], w[7]);
+#pragma unroll
+            for (int dt = 0; dt < DQK / 32; ++dt) {
+                dqacc[dt] = mfma_f16(lds_tr<LK>(aK0, aK1, dt, 32 * t), dsb0, dqacc[dt]);
+                dqacc[dt] = mfma_f16(lds_tr<LK>(aK0, aK1, dt, 32 * t + 16), dsb1, dqacc[dt]);
+            }
+        }
+    }
+
+    if (row_ok) {
+        half_t* dQb = static_cast<half_t*>(p.dq) + row_q * D_qk;
+        if (D_qk == DQK) store_rows_f16<DQK>(dQb, dqacc, p.c.scale, hh);
+        else store_rows_f16_n<DQK>(dQb, dqacc, p.c.scale, hh, D_qk);
+    }
+}
+
+// ===========================================================================
+// Backward, dK/dV kernel (reads stats2 and delta from the workspace)
+// ===========================================================================
+template <int DQK, int DV>
+struct DkvDmaCfg {
+    static constexpr int NT = 256, BKV = 128, BQ = 64;
+    static constexpr int LQ = DQK / 8, LO = DV / 8;
+    static constexpr int QB = BQ * DQK * 2, OB = BQ * DV * 2, FB = 2 * BQ * 4;
+    static constexpr int STAGE = QB + OB + FB;
+    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+};
+
+template <int DQK, int DV, bool CAUSAL, bool DROP>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
+    using Cfg = DkvDmaCfg<DQK, DV>;
+    constexpr int BKV = Cfg::BKV, BQ = Cfg::BQ, LQ = Cfg::LQ, LO = Cfg::LO;
+
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
+    const int tiles = (S_kv + BKV - 1) / BKV;
+    int b, kt;
+    xcd_map(blockIdx.x, B * tiles, tiles, false, b, kt);
+    const int k0 = kt * BKV, kw0 = k0 + 32 * wave, my_k = kw0 + l32;
+    const bool key_ok = my_k < S_kv;
+
+    const half_t* Qb = static_cast<const half_t*>(p.q) + (size_t)b * S_q * D_qk;
+    const half_t* dOb = static_cast<const half_t*>(p.d_o) + (size_t)b * S_q * D_v;
+    const half_t* Kb = static_cast<const half_t*>(p.k) + (size_t)b * S_kv * D_qk;
+    const half_t* Vb = static_cast<const half_t*>(p.v) + (size_t)b * S_kv * D_v;
+    const float* st2b = p.stats2 + (size_t)b * S_q;
+    const float* deltab = p.delta + (size_t)b * S_q;
+
+    // K and V rows of this lane's key as B operands.
+    half8 kreg[DQK / 16], vreg[DV / 16];
+#pragma unroll
+    for (int ks = 0; ks < DQK / 16; ++ks)
+        kreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Kb, my_k, S_kv, 16 * ks + 8 * hh, D_qk, D_qk));
+#pragma unroll
+    for (int ks = 0; ks < DV / 16; ++ks)
+        vreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Vb, my_k, S_kv, 16 * ks + 8 * hh, D_v, D_v));
+
+    // Queries below k0 see none of these keys under the causal mask.
+    const int q_begin = CAUSAL ? (min(k0, S_q) / BQ) * BQ : 0;
+    const int nsteps = (S_q - q_begin + BQ - 1) / BQ;
+
+    TileDma<BQ, LQ> qd;
+    TileDma<BQ, LO> od;
+    qd.init(wave, lane, D_qk * 2, D_qk / 8);
+    od.init(wave, lane, D_v * 2, D_v / 8);
+    auto issue = [&](int step) {
+        const int q0 = q_begin + step * BQ;
+        unsigned char* st = smem + (step & 1) * Cfg::STAGE;
+        qd.issue(make_rsrc(Qb + (size_t)q0 * D_qk, (long long)(S_q - q0) * D_qk * 2), st, wave);
+        od.issue(make_rsrc(dOb + (size_t)q0 * D_v, (long long)(S_q - q0) * D_v * 2), st + Cfg::QB, wave);
+        if (wave == 0) dma4(make_rsrc(st2b + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB, lane * 4);
+        if (wave == 1) dma4(make_rsrc(deltab + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB + BQ * 4, lane * 4);
+    };
+    if (nsteps > 0) issue(0);
+
+    const float sl2 = p.c.scale_log2;
+    const float ksc = p.c.keep_scale;
+    // Dropout: st(q, key) = st(4 hh, key) + q * S_kv * A; the row step is uniform.
+    const uint64_t st_lane = DROP ? lcg_state(p.c.seed_offset, (uint64_t)b * S_q + 4 * hh, (uint64_t)S_kv, my_k) : 0;
+    const uint64_t row_step = (uint64_t)S_kv * kLcgMul;
+    const uint32_t thr = p.c.drop_threshold;
+
+    SwzLane<LQ> swQ;
+    SwzLane<LO> swO;
+    swQ.init(lane);
+    swO.init(lane);
+
+    floatx16 dkacc[DQK / 32], dvacc[DV / 32];
+#pragma unroll
+    for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};
+#pragma unroll
+    for (int dt = 0; dt < DV / 32; ++dt) dvacc[dt] = floatx16{};
+
+    for (int step = 0; step < nsteps; ++step) {
+        wait_vm();
+        __syncthreads();
+        if (step + 1 < nsteps) issue(step + 1);
+        if (kw0 >= S_kv) continue;
+        const int q0 = q_begin + step * BQ;
+        const uint32_t qbase = (uint32_t)((step & 1) * Cfg::STAGE), obase = qbase + Cfg::QB;
+        const uint32_t aQ = qbase + swQ.row, aO = obase + swO.row;
+        const uint32_t aQ0 = qbase + swQ.tr0, aQ1 = qbase + swQ.tr1;
+        const uint32_t aO0 = obase + swO.tr0, aO1 = obase + swO.tr1;
+        const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
+
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int qs = q0 + 32 * t;
+            if (qs >= S_q || (CAUSAL && qs + 31 < kw0)) continue;
+            const bool part = CAUSAL && qs < kw0 + 31;
+
+            floatx16 sacc = floatx16{}, dpacc = floatx16{};
+#pragma unroll
+            for (int ks = 0; ks < DQK / 16; ++ks)
+                sacc = mfma_f16(lds_row<LQ>(aQ, ks, 32 * t), kreg[ks], sacc);
+#pragma unroll
+            for (int ks = 0; ks < DV / 16; ++ks)
+                dpacc = mfma_f16(lds_row<LO>(aO, ks, 32 * t), vreg[ks], dpacc);
+
+            __builtin_amdgcn_sched_barrier(0);
+            // rows of the accumulators are queries qs + 8 g + 4 hh + e
+            const uint64_t st_sub = DROP ? st_lane + (uint64_t)qs * row_step : 0;
+            uint32_t wp[8], wd[8];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int rb = 32 * t + 8 * g + 4 * hh;
+                const floatx4 st4 = *reinterpret_cast<const floatx4*>(Fs + rb);
+                const floatx4 de4 = *reinterpret_cast<const floatx4*>(Fs + BQ + rb);
+                float pk4[4], ds4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * g + e;
+                    float x = __builtin_fmaf(sacc[r], sl2, -st4[e]);
+                    if (part && my_k > qs + 8 * g + 4 * hh + e) x = -INFINITY;
+                    const float pr = fast_exp2(x);
+                    const bool big = pr > kEps;
+                    float pk, tt;
+                    if constexpr (DROP) {
+                        const bool keep = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr);
+                        pk = (big && keep) ? pr : 0.f;
+                        tt = keep ? __builtin_fmaf(dpacc[r], ksc, -de4[e]) : -de4[e];
+                    } else {
+                        pk = big ? pr : 0.f;
+                        tt = dpacc[r] - de4[e];
+                    }
+                    pk4[e] = pk;
+                    ds4[e] = big ? pr * tt : 0.f;
+                }
+                wp[2 * g] = pack_h2(pk4[0], pk4[1]);
+                wp[2 * g + 1] = pack_h2(pk4[2], pk4[3]);
+                wd[2 * g] = pack_h2(ds4[0], ds4[1]);
+                wd[2 * g + 1] = pack_h2(ds4[2], ds4[3]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const half8 pkb0 = half8_of(wp[0], wp[1], wp[2], wp[3]);
+            const half8 pkb1 = half8_of(wp[4], wp[5], wp[6], wp[7]);
+            const half8 dsb0 = half8_of(wd[0], wd[1], wd[2], wd[3]);
+            const half8 dsb1 = half8_of(wd[4], wd[5], wd[6], wd[7]);
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt) {
+                dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t), pkb0, dvacc[dt]);
+                dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t + 16), pkb1, dvacc[dt]);
+            }
+#pragma unroll
+            for (int dt = 0; dt < DQK / 32; ++dt) {
+                dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t), dsb0, dkacc[dt]);
+                dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t + 16), dsb1, dkacc[dt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    if (key_ok) {
+        half_t* dKb = static_cast<half_t*>(p.dk) + ((size_t)b * S_kv + my_k) * D_qk;
+        half_t* dVb = static_cast<half_t*>(p.dv) + ((size_t)b * S_kv + my_k) * D_v;
+        if (D_qk == DQK) store_rows_f16<DQK>(dKb, dkacc, p.c.scale, hh);
+        else store_rows_f16_n<DQK>(dKb, dkacc, p.c.scale, hh, D_qk);
+        if (D_v == DV) store_rows_f16<DV>(dVb, dvacc, p.c.keep_scale, hh);
+        else store_rows_f16_n<DV>(dVb, dvacc, p.c.keep_scale, hh, D_v);
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_fwd_f16_dma(const FwdParams& p, hipStream_t stream) {
+    const int B = p.s.B, S_q = p.s.S_q;
+    if (B == 0 || S_q == 0) return hipSuccess;
+    return with_dim(p.s.D_qk, [&](auto dqk) {
+        return with_dim(p.s.D_v, [&](auto dv) {
+            return with_bool(p.c.causal != 0, [&](auto c) {
+                return with_bool(p.c.use_dropout != 0, [&](auto d) {
+                    constexpr int DQK = decltype(dqk)::value, DV = decltype(dv)::value;
+                    using Cfg = FwdDmaCfg<DQK, DV>;
+                    const long long n = (long long)((S_q + Cfg::BM - 1) / Cfg::BM) * B;
+                    return launch_kernel<sdpa_fwd_f16_dma_kernel<DQK, DV, decltype(c)::value, decltype(d)::value>>(
+                        (unsigned)n, Cfg::NT, Cfg::LDS_BYTES, stream, p);
+                });
+            });
+        });
+    });
+}
+
+hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream) {
+    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv;
+    if (B == 0) return hipSuccess;
+    return with_dim(p.s.D_qk, [&](auto dqk) {
+        return with_dim(p.s.D_v, [&](auto dv) {
+            return with_bool(p.c.causal != 0, [&](auto c) {
+                return with_bool(p.c.use_dropout != 0, [&](auto d) {
+                    constexpr int DQK = decltype(dqk)::value, DV = decltype(dv)::value;
+                    constexpr bool CA = decltype(c)::value, DR = decltype(d)::value;
+                    using CQ = DqDmaCfg<DQK, DV>;
+                    using CK = DkvDmaCfg<DQK, DV>;
+                    hipError_t err = hipSuccess;
+                    if ((phases & kBwdDq) && S_q > 0) {
+                        const long long n = (long long)((S_q + CQ::BM - 1) / CQ::BM) * B;
+                        err = launch_kernel<sdpa_bwd_dq_f16_dma_kernel<DQK, DV, CA, DR>>((unsigned)n, CQ::NT,
+                                                                                   CQ::LDS_BYTES, stream, p);
+                    }
+                    if (err == hipSuccess && (phases & kBwdDkDv) && S_kv > 0) {
+                        const long long n = (long long)((S_kv + CK::BKV - 1) / CK::BKV) * B;
+                        err = launch_kernel<sdpa_bwd_dkdv_f16_dma_kernel<DQK, DV, CA, DR>>((unsigned)n, CK::NT,
+                                                                                     CK::LDS_BYTES, stream, p);
+                    }
+                    return err;
+                });
+            });
+        });
+    });
+}
+
+}  // namespace sdpa

@@ -1,7 +1,7 @@
 // sdpa_params.h -- kernel argument blocks shared by the host launchers and the
 // HIP kernels.  Every tensor is dense row-major [B, S, D] (reference indexing
 // (batch_offset + s) * d_size + d, sdpa/sdpa_utils.cuh:41); stats and the
-// backward's delta are fp32 [B, S_q].
+// backward's workspace rows (stats2, delta) are fp32 [B, S_q].
 #pragma once
 
 #include <stdint.h>
@@ -43,7 +43,9 @@ struct BwdParams {
     void* dq;
     void* dk;
     void* dv;
-    float* delta;  // workspace [B, S_q]: delta_i = sum_d dO[i,d] * O[i,d]
+    // Workspace, written by the dQ kernel and read by the dK/dV kernel:
+    float* stats2;  // [B, S_q]: stats_i * log2(e)
+    float* delta;   // [B, S_q]: delta_i = sum_d dO[i,d] * O[i,d]
     AttnShape s;
     AttnScalars c;
 };
