@@ -527,10 +527,13 @@ struct DkvDmaCfg {
     static constexpr int QB = BQ * DQK * 2, OB = BQ * DV * 2, FB = 2 * BQ * 4;
     static constexpr int STAGE = QB + OB + FB;
     static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+    // waves per SIMD: K, V, dK and dV of 32 keys at D = 128 plus the step's
+    // working set do not fit in 256 VGPRs, so that shape runs one wave per SIMD.
+    static constexpr int WAVES = (DQK == 128 && DV == 128) ? 1 : 2;
 };
 
 template <int DQK, int DV, bool CAUSAL, bool DROP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DkvDmaCfg<DQK, DV>::WAVES, DkvDmaCfg<DQK, DV>::WAVES)))
 void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     using Cfg = DkvDmaCfg<DQK, DV>;
     constexpr int BKV = Cfg::BKV, BQ = Cfg::BQ, LQ = Cfg::LQ, LO = Cfg::LO;
@@ -560,16 +563,20 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     for (int ks = 0; ks < DV / 16; ++ks)
         vreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Vb, my_k, S_kv, 16 * ks + 8 * hh, D_v, D_v));
 
-    // Queries below k0 see none of these keys under the causal mask.
+    // Queries below k0 see none of these keys under the causal mask.  The
+    // query blocks are walked top-down: every key tile of a batch row starts
+    // at the same (last) block and they move down together, so concurrent
+    // workgroups read the same Q/dO rows while they are in L2.
     const int q_begin = CAUSAL ? (min(k0, S_q) / BQ) * BQ : 0;
     const int nsteps = (S_q - q_begin + BQ - 1) / BQ;
+    const int q_top = q_begin + (nsteps - 1) * BQ;
 
     TileDma<BQ, LQ> qd;
     TileDma<BQ, LO> od;
     qd.init(wave, lane, D_qk * 2, D_qk / 8);
     od.init(wave, lane, D_v * 2, D_v / 8);
     auto issue = [&](int step) {
-        const int q0 = q_begin + step * BQ;
+        const int q0 = q_top - step * BQ;
         unsigned char* st = smem + (step & 1) * Cfg::STAGE;
         qd.issue(make_rsrc(Qb + (size_t)q0 * D_qk, (long long)(S_q - q0) * D_qk * 2), st, wave);
         od.issue(make_rsrc(dOb + (size_t)q0 * D_v, (long long)(S_q - q0) * D_v * 2), st + Cfg::QB, wave);
@@ -601,7 +608,7 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
         __syncthreads();
         if (step + 1 < nsteps) issue(step + 1);
         if (kw0 >= S_kv) continue;
-        const int q0 = q_begin + step * BQ;
+        const int q0 = q_top - step * BQ;
         const uint32_t qbase = (uint32_t)((step & 1) * Cfg::STAGE), obase = qbase + Cfg::QB;
         const uint32_t aQ = qbase + swQ.row, aO = obase + swO.row;
         const uint32_t aQ0 = qbase + swQ.tr0, aQ1 = qbase + swQ.tr1;
@@ -621,7 +628,14 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
 #pragma unroll
             for (int ks = 0; ks < DV / 16; ++ks)
                 dpacc = mfma_f16(lds_row<LO>(aO, ks, 32 * t), vreg[ks], dpacc);
-
+            // keep at most two operand reads ahead of the MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int i = 0; i < (DQK + DV) / 16 - 2; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             __builtin_amdgcn_sched_barrier(0);
             // rows of the accumulators are queries qs + 8 g + 4 hh + e
             const uint64_t st_sub = DROP ? st_lane + (uint64_t)qs * row_step : 0;
@@ -671,6 +685,14 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
                 dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t), dsb0, dkacc[dt]);
                 dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t + 16), dsb1, dkacc[dt]);
             }
+            // each MFMA takes two transposed reads; keep two MFMAs' worth ahead
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+            for (int i = 0; i < (DQK + DV) / 16 - 2; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
