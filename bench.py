@@ -120,7 +120,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-rows", type=int, default=256,
+    ap.add_argument("--cpu-rows", type=int, default=512,
                     help="query rows per batch in the CPU baseline sample (0: skip it)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0: auto)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,

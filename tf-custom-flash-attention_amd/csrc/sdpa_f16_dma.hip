@@ -33,6 +33,8 @@
 // Element semantics are those of the reference (sdpa/sdpa_fwd.cu.cc:93-173,
 // sdpa/sdpa_bwd.cu.cc:130-170, 291-327), restated in sdpa_fwd.hip and
 // sdpa_bwd.hip.
+#include <type_traits>
+
 #include "sdpa_device.h"
 #include "sdpa_launch.h"
 #include "sdpa_params.h"
@@ -65,17 +67,19 @@ __device__ __forceinline__ void dma4(rsrc_t r, unsigned char* wave_dst, uint32_t
 // s_waitcnt vmcnt(0): this wave's copies (and loads) have landed.
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Per-lane global offsets of one ROWS x (8 L) fp16 tile copied by 4 waves.
-// LDS chunk slot p (16 bytes) of the tile is row p / L, position p % L; it
-// receives global chunk (p % L) ^ swz<L>(row) of that row.  Copy u of wave w
-// fills slots (4 u + w) * 64 + lane, i.e. rows (4 u + w) * 64 / L + lane / L;
-// for every L the swizzle term of those rows does not depend on u, so one
-// offset per lane plus u * (256 / L) rows covers all of the wave's copies.
-template <int ROWS, int L>
+// Per-lane global offsets of one ROWS x (8 L) fp16 tile copied by NW waves
+// (NW = 4 or 8).  LDS chunk slot p (16 bytes) of the tile is row p / L,
+// position p % L; it receives global chunk (p % L) ^ swz<L>(row) of that row.
+// Copy u of wave w fills slots (NW u + w) * 64 + lane, i.e. rows
+// (NW u + w) * 64 / L + lane / L; for NW in {4, 8} and every L the swizzle
+// term of those rows does not depend on u, so one offset per lane plus
+// u * NW * 64 / L rows covers all of the wave's copies.
+template <int ROWS, int L, int NW>
 struct TileDma {
     static constexpr int LOADS = ROWS * L / 64;  // wave-sized copies per tile
-    static constexpr int PER_WAVE = LOADS / 4;
-    static_assert(LOADS % 4 == 0, "a tile is split evenly over the 4 waves");
+    static constexpr int PER_WAVE = (LOADS + NW - 1) / NW;
+    static constexpr int MIN_PER_WAVE = LOADS / NW;  // copies issued by every wave
+    static_assert(NW == 4 || NW == 8, "swizzle term is copy-invariant for 4 or 8 waves");
     uint32_t voff0;     // offset of copy 0, or kOob for chunks past D
     uint32_t row_step;  // bytes between consecutive copies of a wave
 
@@ -85,13 +89,22 @@ struct TileDma {
         const int r = slot / L;
         const int c = (slot % L) ^ swz<L>(r);
         voff0 = c < valid_chunks ? (uint32_t)(r * row_bytes + c * 16) : kOob;
-        row_step = (uint32_t)((256 / L) * row_bytes);
+        row_step = (uint32_t)((NW * 64 / L) * row_bytes);
     }
     __device__ __forceinline__ void issue(rsrc_t rs, unsigned char* tile, int wave) const {
 #pragma unroll
-        for (int u = 0; u < PER_WAVE; ++u) dma16(rs, tile + (u * 4 + wave) * 1024, voff0 + u * row_step);
+        for (int u = 0; u < PER_WAVE; ++u)
+            if (LOADS % NW == 0 || u * NW + wave < LOADS)
+                dma16(rs, tile + (u * NW + wave) * 1024, voff0 + u * row_step);
     }
 };
+
+// s_waitcnt vmcnt(N): at most N of this wave's loads still in flight.
+template <int N>
+__device__ __forceinline__ void wait_vm_n() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 // Workgroup id -> (batch, tile), XCD-major: XCD x (ids x, x+8, ...) owns a
 // contiguous range of the batch-major tile list.  `reverse` issues the tiles
@@ -198,14 +211,23 @@ __device__ __forceinline__ void store_rows_f16_n(half_t* dst, const floatx16 (&a
 // ===========================================================================
 template <int DQK, int DV>
 struct FwdDmaCfg {
-    static constexpr int NT = 256, BM = 128, BN = 64;
+    // NW waves of 32 queries each; K/V blocks of BN keys in an NSTAGE-deep
+    // LDS ring (the copy of block n + NSTAGE - 1 is issued at step n).
+#ifndef SDPA_FWD_NW
+#define SDPA_FWD_NW 4
+#endif
+#ifndef SDPA_FWD_NSTAGE
+#define SDPA_FWD_NSTAGE 2
+#endif
+    static constexpr int NW = SDPA_FWD_NW, NSTAGE = SDPA_FWD_NSTAGE;
+    static constexpr int NT = 64 * NW, BM = 32 * NW, BN = 64;
     static constexpr int LK = DQK / 8, LV = DV / 8;
     static constexpr int KB = BN * DQK * 2, VB = BN * DV * 2, STAGE = KB + VB;
-    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+    static constexpr size_t LDS_BYTES = NSTAGE * (size_t)STAGE;
 };
 
 template <int DQK, int DV, bool CAUSAL, bool DROP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__((FwdDmaCfg<DQK, DV>::NT)) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
     using Cfg = FwdDmaCfg<DQK, DV>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV;
@@ -237,19 +259,24 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         qreg[ks] = neg ? -v : v;
     }
 
-    TileDma<BN, LK> kd;
-    TileDma<BN, LV> vd;
+    constexpr int NW = Cfg::NW, NSTAGE = Cfg::NSTAGE;
+    TileDma<BN, LK, NW> kd;
+    TileDma<BN, LV, NW> vd;
+    // copies issued by every wave per step (waits count only those)
+    constexpr int LPS = TileDma<BN, LK, NW>::MIN_PER_WAVE + TileDma<BN, LV, NW>::MIN_PER_WAVE;
     kd.init(wave, lane, D_qk * 2, D_qk / 8);
     vd.init(wave, lane, D_v * 2, D_v / 8);
     const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
     const int nsteps = (kv_end + BN - 1) / BN;
     auto issue = [&](int step) {
         const int kv0 = step * BN;
-        unsigned char* st = smem + (step & 1) * Cfg::STAGE;
+        unsigned char* st = smem + (step % NSTAGE) * Cfg::STAGE;
         kd.issue(make_rsrc(Kb + (size_t)kv0 * D_qk, (long long)(S_kv - kv0) * D_qk * 2), st, wave);
         vd.issue(make_rsrc(Vb + (size_t)kv0 * D_v, (long long)(S_kv - kv0) * D_v * 2), st + Cfg::KB, wave);
     };
-    if (nsteps > 0) issue(0);
+#pragma unroll
+    for (int i = 0; i < NSTAGE - 1; ++i)
+        if (i < nsteps) issue(i);
 
     floatx16 oacc[DV / 32];
 #pragma unroll
@@ -265,96 +292,175 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
     swK.init(lane);
     swV.init(lane);
 
-    for (int step = 0; step < nsteps; ++step) {
-        wait_vm();
-        __syncthreads();
-        if (step + 1 < nsteps) issue(step + 1);
-        if (qw0 >= S_q) continue;
-        const int kv0 = step * BN;
-        const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE), vbase = kbase + Cfg::KB;
-        const uint32_t aK = kbase + swK.row, aV0 = vbase + swV.tr0, aV1 = vbase + swV.tr1;
-
-        // 32-key sub-tiles: live (any visible key) and part (needs masking).
-        bool live[2], part[2];
+    // Softmax of one 32-key sub-tile t (scores s, raw q.k; masked keys set to
+    // -inf by the caller): per-lane lazy maximum m_use (moves only when the
+    // block maximum exceeds the running one by more than 2^kTauF), alpha =
+    // exp2(m_run - m_use), P = exp2(s sl2 - m_use), the undropped sum and the
+    // dropped, fp16-packed B operands of the PV product.
+    auto softmax_sub = [&](const floatx16& sc, int t, uint64_t st_blk, float& m_use, float& alpha, float& lsum,
+                           half8& pb0, half8& pb1) {
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int k0 = kv0 + 32 * t;
-            live[t] = k0 < S_kv && (!CAUSAL || k0 <= qw0 + 31);
-            part[t] = k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0);
-        }
-
-        // ---- S^T = K Q^T ------------------------------------------------
-        floatx16 s[2];
+        for (int r = 3; r < 15; r += 2) mx = fmaxf(mx, fmaxf(sc[r], sc[r + 1]));
+        mx = fmaxf(mx, sc[15]);
+        mx = xhalf_max(mx) * sl2;
+        m_use = (mx > m_run + kTauF) ? fmaxf(m_run, mx) : m_run;
+        alpha = fast_exp2(m_run - m_use);
+        const float nm = -m_use;
+        uint32_t w[8];
+        float lq[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            s[t] = floatx16{};
-            if (live[t]) {
+        for (int r = 0; r < 16; r += 4) {
+            float pq[4];
 #pragma unroll
-                for (int ks = 0; ks < DQK / 16; ++ks)
-                    s[t] = mfma_f16(lds_row<LK>(aK, ks, 32 * t), qreg[ks], s[t]);
-                if (part[t]) {
+            for (int e = 0; e < 4; ++e) pq[e] = fast_exp2(__builtin_fmaf(sc[r + e], sl2, nm));
+            lq[r >> 2] = (pq[0] + pq[1]) + (pq[2] + pq[3]);
+            if constexpr (DROP) {
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * hh + (r & 3);
-                        if (key >= S_kv || (CAUSAL && key > my_q)) s[t][r] = -INFINITY;
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    const int c = 32 * t + 8 * (r >> 2) + e;
+                    pq[e] = lcg_keep(st_blk + (uint64_t)c * kLcgMul, thr) ? pq[e] : 0.f;
                 }
             }
+            w[r >> 1] = pack_h2(pq[0], pq[1]);
+            w[(r >> 1) + 1] = pack_h2(pq[2], pq[3]);
         }
-
-        // ---- running maximum (raw scores), lazy rescale --------------------
-        float mx = -INFINITY;
+        lsum = (lq[0] + lq[1]) + (lq[2] + lq[3]);
+        pb0 = half8_of(w[0], w[1], w[2], w[3]);
+        pb1 = half8_of(w[4], w[5], w[6], w[7]);
+    };
+    // Mask of sub-tile t: keys past S_kv and, causal, keys after the query.
+    auto mask_sub = [&](floatx16& sc, int kv0, int t) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-            if (live[t])
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[t][r], s[t][r + 1]));
-        mx = xhalf_max(mx) * sl2;
-        if (wave_any(mx > m_run + kTauF)) {
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = fast_exp2(m_run - m_new);
-            l_run *= alpha;
+        for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * hh + (r & 3);
+            if (key >= S_kv || (CAUSAL && key > my_q)) sc[r] = -INFINITY;
+        }
+    };
+    // After a sub-tile's PV operands are formed: rescale the output (rare,
+    // wave-uniform branch) and fold the sub-tile into the running sum.
+    auto commit_sub = [&](float m_use, float alpha, float lsum) {
+        if (wave_any(alpha != 1.f)) {
 #pragma unroll
             for (int dt = 0; dt < DV / 32; ++dt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-            m_run = m_new;
         }
+        l_run = __builtin_fmaf(l_run, alpha, lsum);
+        m_run = m_use;
+    };
 
-        // ---- P = exp2(s*sl2 - m), undropped sum, dropout, fp16 B operands ---
-        const float nm = -m_run;
+    // One step = 64 keys as two 32-key sub-tiles, software-pipelined so that
+    // every MFMA group has independent work interleaved with it (a wave
+    // issues in order: VALU work placed after a run of MFMAs waits for them):
+    //   R1  S(0) = K0 Q^T           || LDS reads of K1
+    //   R2  S(1) = K1 Q^T           || softmax(0), LDS reads of V0^T
+    //   R3  O^T += V0^T P0~^T       || softmax(1), LDS reads of V1^T
+    //   R4  O^T += V1^T P1~^T
+    // The rescale of O by sub-tile 1's new maximum commutes with the pending
+    // PV(0) accumulation, so it is applied after R3.
+    auto fwd_step = [&]<bool PART>(int kv0, uint32_t aK, uint32_t aV0, uint32_t aV1) {
+        const bool part0 = PART && (kv0 + 32 > S_kv || (CAUSAL && kv0 + 31 > qw0));
+        const bool part1 = PART && (kv0 + 64 > S_kv || (CAUSAL && kv0 + 63 > qw0));
         const uint64_t st_blk = DROP ? st_lane + (uint64_t)kv0 * kLcgMul : 0;
-        half8 pb[4];
-        float ls[4] = {0.f, 0.f, 0.f, 0.f};
+        half8 ak0[DQK / 16], ak1[DQK / 16];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (!live[t]) continue;
-            uint32_t w[8];
+        for (int ks = 0; ks < DQK / 16; ++ks) ak0[ks] = lds_row<LK>(aK, ks, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // R1
+        floatx16 s0 = floatx16{}, s1 = floatx16{};
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                float p0 = fast_exp2(__builtin_fmaf(s[t][r], sl2, nm));
-                float p1 = fast_exp2(__builtin_fmaf(s[t][r + 1], sl2, nm));
-                ls[(r >> 2) & 3] += p0 + p1;
-                if constexpr (DROP) {
-                    const int c0 = 32 * t + 8 * (r >> 2) + (r & 3);
-                    p0 = lcg_keep(st_blk + (uint64_t)c0 * kLcgMul, thr) ? p0 : 0.f;
-                    p1 = lcg_keep(st_blk + (uint64_t)(c0 + 1) * kLcgMul, thr) ? p1 : 0.f;
-                }
-                w[r >> 1] = pack_h2(p0, p1);
+        for (int ks = 0; ks < DQK / 16; ++ks) {
+            s0 = mfma_f16(ak0[ks], qreg[ks], s0);
+            ak1[ks] = lds_row<LK>(aK, ks, 32);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // R2
+#pragma unroll
+        for (int ks = 0; ks < DQK / 16; ++ks) s1 = mfma_f16(ak1[ks], qreg[ks], s1);
+        half8 av0[2][DV / 32], av1[2][DV / 32];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt) av0[j][dt] = lds_tr<LV>(aV0, aV1, dt, 16 * j);
+        if (part0) mask_sub(s0, kv0, 0);
+        float mu0, al0, ls0;
+        half8 p00, p01;
+        softmax_sub(s0, 0, st_blk, mu0, al0, ls0, p00, p01);
+        // pin sub-tile 0's softmax inside R2 (its results are used only after
+        // the rescale branch, which would otherwise let them sink below it)
+        asm volatile("" ::"v"(p00), "v"(p01), "v"(ls0), "v"(mu0), "v"(al0));
+        if constexpr (!PART) {
+#pragma unroll
+            for (int i = 0; i < DQK / 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2 * (2 * DV / 32) / (DQK / 16) > 0 ? 2 * (2 * DV / 32) / (DQK / 16) : 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
             }
-            pb[2 * t] = half8_of(w[0], w[1], w[2], w[3]);
-            pb[2 * t + 1] = half8_of(w[4], w[5], w[6], w[7]);
         }
-        l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        __builtin_amdgcn_sched_barrier(0);
+        commit_sub(mu0, al0, ls0);
+        __builtin_amdgcn_sched_barrier(0);
+        // R3
+#pragma unroll
+        for (int dt = 0; dt < DV / 32; ++dt) {
+            oacc[dt] = mfma_f16(av0[0][dt], p00, oacc[dt]);
+            oacc[dt] = mfma_f16(av0[1][dt], p01, oacc[dt]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt) av1[j][dt] = lds_tr<LV>(aV0, aV1, dt, 32 + 16 * j);
+        if (part1) mask_sub(s1, kv0, 1);
+        float mu1, al1, ls1;
+        half8 p10, p11;
+        softmax_sub(s1, 1, st_blk, mu1, al1, ls1, p10, p11);
+        asm volatile("" ::"v"(p10), "v"(p11), "v"(ls1), "v"(mu1), "v"(al1));
+        if constexpr (!PART) {
+#pragma unroll
+            for (int i = 0; i < 2 * DV / 32; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        commit_sub(mu1, al1, ls1);
+        __builtin_amdgcn_sched_barrier(0);
+        // R4
+#pragma unroll
+        for (int dt = 0; dt < DV / 32; ++dt) {
+            oacc[dt] = mfma_f16(av1[0][dt], p10, oacc[dt]);
+            oacc[dt] = mfma_f16(av1[1][dt], p11, oacc[dt]);
+        }
+    };
 
-        // ---- O^T += V^T P~^T ----------------------------------------------
-#pragma unroll
-        for (int sk = 0; sk < 4; ++sk) {
-            if (!live[sk >> 1]) continue;
-#pragma unroll
-            for (int dt = 0; dt < DV / 32; ++dt)
-                oacc[dt] = mfma_f16(lds_tr<LV>(aV0, aV1, dt, 16 * sk), pb[sk], oacc[dt]);
-        }
+    // Wait for block `step` (at most the copies of the NSTAGE - 2 later blocks
+    // may still be in flight; all of them at the tail), synchronise, and start
+    // the copy of block step + NSTAGE - 1.
+    auto sync_step = [&](int step) {
+        if (step + NSTAGE - 2 < nsteps) wait_vm_n<(NSTAGE - 2) * LPS>();
+        else wait_vm();
+        __syncthreads();
+        if (step + NSTAGE - 1 < nsteps) issue(step + NSTAGE - 1);
+    };
+    // Steps whose 64 keys are all visible to all 32 queries of this wave run
+    // the unmasked variant; the causal diagonal and the key tail come last.
+    const int full_lim = CAUSAL ? min(qw0 - (BN - 1), S_kv - BN) : S_kv - BN;
+    const int n_full = qw0 >= S_q ? 0 : min(nsteps, full_lim < 0 ? 0 : full_lim / BN + 1);
+    const bool live = qw0 < S_q;
+    int step = 0;
+    for (; step < n_full; ++step) {
+        sync_step(step);
+        const uint32_t kbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE), vbase = kbase + Cfg::KB;
+        fwd_step.template operator()<false>(step * BN, kbase + swK.row, vbase + swV.tr0, vbase + swV.tr1);
+    }
+    for (; step < nsteps; ++step) {
+        sync_step(step);
+        const int kv0 = step * BN;
+        if (!live || (CAUSAL && kv0 > qw0 + 31)) continue;  // no visible key in this step
+        const uint32_t kbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE), vbase = kbase + Cfg::KB;
+        fwd_step.template operator()<true>(kv0, kbase + swK.row, vbase + swV.tr0, vbase + swV.tr1);
     }
 
     // ---- epilogue: stats = m + log(l + 1e-6), O = acc / l (0 if l <= 1e-6) ----
@@ -424,8 +530,8 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
     const float ksc = p.c.keep_scale;
     const float nst = -stats2;
 
-    TileDma<BN, LK> kd;
-    TileDma<BN, LV> vd;
+    TileDma<BN, LK, 4> kd;
+    TileDma<BN, LV, 4> vd;
     kd.init(wave, lane, D_qk * 2, D_qk / 8);
     vd.init(wave, lane, D_v * 2, D_v / 8);
     const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
@@ -571,8 +677,8 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     const int nsteps = (S_q - q_begin + BQ - 1) / BQ;
     const int q_top = q_begin + (nsteps - 1) * BQ;
 
-    TileDma<BQ, LQ> qd;
-    TileDma<BQ, LO> od;
+    TileDma<BQ, LQ, 4> qd;
+    TileDma<BQ, LO, 4> od;
     qd.init(wave, lane, D_qk * 2, D_qk / 8);
     od.init(wave, lane, D_v * 2, D_v / 8);
     auto issue = [&](int step) {
