@@ -92,9 +92,13 @@ struct TileDma {
         row_step = (uint32_t)((NW * 64 / L) * row_bytes);
     }
     __device__ __forceinline__ void issue(rsrc_t rs, unsigned char* tile, int wave) const {
+        issue_part(rs, tile, wave, 0, PER_WAVE);
+    }
+    // copies u0 <= u < u1 only (to spread a tile's copies over a step)
+    __device__ __forceinline__ void issue_part(rsrc_t rs, unsigned char* tile, int wave, int u0, int u1) const {
 #pragma unroll
         for (int u = 0; u < PER_WAVE; ++u)
-            if (LOADS % NW == 0 || u * NW + wave < LOADS)
+            if (u >= u0 && u < u1 && (LOADS % NW == 0 || u * NW + wave < LOADS))
                 dma16(rs, tile + (u * NW + wave) * 1024, voff0 + u * row_step);
     }
 };
@@ -632,10 +636,12 @@ struct DkvDmaCfg {
     static constexpr int LQ = DQK / 8, LO = DV / 8;
     static constexpr int QB = BQ * DQK * 2, OB = BQ * DV * 2, FB = 2 * BQ * 4;
     static constexpr int STAGE = QB + OB + FB;
-    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
-    // waves per SIMD: K, V, dK and dV of 32 keys at D = 128 plus the step's
-    // working set do not fit in 256 VGPRs, so that shape runs one wave per SIMD.
-    static constexpr int WAVES = (DQK == 128 && DV == 128) ? 1 : 2;
+    // waves per SIMD: with a 128-wide side, K, V, dK and dV of 32 keys plus
+    // the step's working set do not fit in 256 VGPRs, so those shapes run one
+    // wave per SIMD (one workgroup per CU, which leaves LDS for a deeper ring).
+    static constexpr int WAVES = (DQK == 128 || DV == 128) ? 1 : 2;
+    static constexpr int NSTAGE = (WAVES == 1 || 3 * STAGE <= 80 * 1024) ? 3 : 2;
+    static constexpr size_t LDS_BYTES = NSTAGE * (size_t)STAGE;
 };
 
 template <int DQK, int DV, bool CAUSAL, bool DROP>
@@ -677,19 +683,32 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     const int nsteps = (S_q - q_begin + BQ - 1) / BQ;
     const int q_top = q_begin + (nsteps - 1) * BQ;
 
+    constexpr int NSTAGE = Cfg::NSTAGE;
     TileDma<BQ, LQ, 4> qd;
     TileDma<BQ, LO, 4> od;
+    // copies issued by every wave per step (waves 0 and 1 add one each)
+    constexpr int LPS = TileDma<BQ, LQ, 4>::MIN_PER_WAVE + TileDma<BQ, LO, 4>::MIN_PER_WAVE;
     qd.init(wave, lane, D_qk * 2, D_qk / 8);
     od.init(wave, lane, D_v * 2, D_v / 8);
     auto issue = [&](int step) {
         const int q0 = q_top - step * BQ;
-        unsigned char* st = smem + (step & 1) * Cfg::STAGE;
+        unsigned char* st = smem + (step % NSTAGE) * Cfg::STAGE;
         qd.issue(make_rsrc(Qb + (size_t)q0 * D_qk, (long long)(S_q - q0) * D_qk * 2), st, wave);
         od.issue(make_rsrc(dOb + (size_t)q0 * D_v, (long long)(S_q - q0) * D_v * 2), st + Cfg::QB, wave);
         if (wave == 0) dma4(make_rsrc(st2b + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB, lane * 4);
         if (wave == 1) dma4(make_rsrc(deltab + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB + BQ * 4, lane * 4);
     };
-    if (nsteps > 0) issue(0);
+#pragma unroll
+    for (int i = 0; i < NSTAGE - 1; ++i)
+        if (i < nsteps) issue(i);
+    // Wait for block `step` (the copies of the NSTAGE - 2 later blocks may
+    // still fly; all of them at the tail), synchronise, start the next copy.
+    auto sync_step = [&](int step) {
+        if (step + NSTAGE - 2 < nsteps) wait_vm_n<(NSTAGE - 2) * LPS>();
+        else wait_vm();
+        __syncthreads();
+        if (step + NSTAGE - 1 < nsteps) issue(step + NSTAGE - 1);
+    };
 
     const float sl2 = p.c.scale_log2;
     const float ksc = p.c.keep_scale;
@@ -709,97 +728,213 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
 #pragma unroll
     for (int dt = 0; dt < DV / 32; ++dt) dvacc[dt] = floatx16{};
 
-    for (int step = 0; step < nsteps; ++step) {
-        wait_vm();
-        __syncthreads();
-        if (step + 1 < nsteps) issue(step + 1);
-        if (kw0 >= S_kv) continue;
-        const int q0 = q_top - step * BQ;
-        const uint32_t qbase = (uint32_t)((step & 1) * Cfg::STAGE), obase = qbase + Cfg::QB;
+    // Element-wise part of one 32-query sub-tile: the accumulator rows are
+    // queries qs + 8 g + 4 hh + e; st4 / de4 hold their stats * log2(e) and
+    // delta.  Produces the fp16 B operands P~ (for dV) and dS (for dK).
+    auto elem = [&]<bool MASK>(const floatx16& sacc, const floatx16& dpacc, const floatx4 (&st4)[4],
+                               const floatx4 (&de4)[4], int qs, half8& pk0, half8& pk1, half8& ds0, half8& ds1) {
+        const uint64_t st_sub = DROP ? st_lane + (uint64_t)qs * row_step : 0;
+        uint32_t wp[8], wd[8];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float pk4[4], ds4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int r = 4 * g + e;
+                float x = __builtin_fmaf(sacc[r], sl2, -st4[g][e]);
+                if (MASK && my_k > qs + 8 * g + 4 * hh + e) x = -INFINITY;
+                float pr = fast_exp2(x);
+                pr = pr > kEps ? pr : 0.f;
+                if constexpr (DROP) {
+                    const bool keep = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr);
+                    pk4[e] = keep ? pr : 0.f;
+                    ds4[e] = pr * (keep ? __builtin_fmaf(dpacc[r], ksc, -de4[g][e]) : -de4[g][e]);
+                } else {
+                    pk4[e] = pr;
+                    ds4[e] = pr * (dpacc[r] - de4[g][e]);
+                }
+            }
+            wp[2 * g] = pack_h2(pk4[0], pk4[1]);
+            wp[2 * g + 1] = pack_h2(pk4[2], pk4[3]);
+            wd[2 * g] = pack_h2(ds4[0], ds4[1]);
+            wd[2 * g + 1] = pack_h2(ds4[2], ds4[3]);
+        }
+        pk0 = half8_of(wp[0], wp[1], wp[2], wp[3]);
+        pk1 = half8_of(wp[4], wp[5], wp[6], wp[7]);
+        ds0 = half8_of(wd[0], wd[1], wd[2], wd[3]);
+        ds1 = half8_of(wd[4], wd[5], wd[6], wd[7]);
+    };
+    auto read_f = [&](const float* Fs, int t, floatx4 (&st4)[4], floatx4 (&de4)[4]) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            st4[g] = *reinterpret_cast<const floatx4*>(Fs + 32 * t + 8 * g + 4 * hh);
+            de4[g] = *reinterpret_cast<const floatx4*>(Fs + BQ + 32 * t + 8 * g + 4 * hh);
+        }
+    };
+
+    // One step of 64 queries whose two 32-query sub-tiles are fully visible
+    // to the wave's keys, software-pipelined (a wave issues in order, so the
+    // element-wise work of one sub-tile is interleaved with the MFMAs of
+    // another):
+    //   R1  A(0): S, dP of sub-tile 0           || reads of A(1) operands, F(0)
+    //   R2  A(1)                                 || B(0) elementwise, reads of C(0) operands, F(1)
+    //   R3  C(0): dV += dO0^T P0~, dK += Q0^T dS0 || B(1), reads of C(1) operands
+    //   R4  C(1)
+    constexpr int NK = DQK / 16, NV = DV / 16, NA = NK > NV ? NK : NV;
+    auto full_step = [&](uint32_t qbase, int q0) {
+        const uint32_t obase = qbase + Cfg::QB;
+        const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
         const uint32_t aQ = qbase + swQ.row, aO = obase + swO.row;
         const uint32_t aQ0 = qbase + swQ.tr0, aQ1 = qbase + swQ.tr1;
         const uint32_t aO0 = obase + swO.tr0, aO1 = obase + swO.tr1;
-        const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
+        half8 aq0[NK], ao0[NV], aq1[NK], ao1[NV];
+#pragma unroll
+        for (int ks = 0; ks < NA; ++ks) {
+            if (ks < NK) aq0[ks] = lds_row<LQ>(aQ, ks, 0);
+            if (ks < NV) ao0[ks] = lds_row<LO>(aO, ks, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- R1
+        floatx16 s0 = floatx16{}, d0 = floatx16{}, s1 = floatx16{}, d1 = floatx16{};
+#pragma unroll
+        for (int ks = 0; ks < NA; ++ks) {
+            if (ks < NK) s0 = mfma_f16(aq0[ks], kreg[ks], s0);
+            if (ks < NV) d0 = mfma_f16(ao0[ks], vreg[ks], d0);
+        }
+#pragma unroll
+        for (int ks = 0; ks < NA; ++ks) {
+            if (ks < NK) aq1[ks] = lds_row<LQ>(aQ, ks, 32);
+            if (ks < NV) ao1[ks] = lds_row<LO>(aO, ks, 32);
+        }
+        floatx4 f0s[4], f0d[4], f1s[4], f1d[4];
+        read_f(Fs, 0, f0s, f0d);
+#pragma unroll
+        for (int i = 0; i < NK + NV; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- R2
+#pragma unroll
+        for (int ks = 0; ks < NA; ++ks) {
+            if (ks < NK) s1 = mfma_f16(aq1[ks], kreg[ks], s1);
+            if (ks < NV) d1 = mfma_f16(ao1[ks], vreg[ks], d1);
+        }
+        half8 cv0[2][DV / 32], cq0[2][DQK / 32], cv1[2][DV / 32], cq1[2][DQK / 32];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt) cv0[j][dt] = lds_tr<LO>(aO0, aO1, dt, 16 * j);
+#pragma unroll
+            for (int dt = 0; dt < DQK / 32; ++dt) cq0[j][dt] = lds_tr<LQ>(aQ0, aQ1, dt, 16 * j);
+        }
+        read_f(Fs, 1, f1s, f1d);
+        half8 pk00, pk01, ds00, ds01;
+        elem.template operator()<false>(s0, d0, f0s, f0d, q0, pk00, pk01, ds00, ds01);
+        asm volatile("" ::"v"(pk00), "v"(pk01), "v"(ds00), "v"(ds01));
+#pragma unroll
+        for (int i = 0; i < NK + NV; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- R3
+#pragma unroll
+        for (int dt = 0; dt < DV / 32; ++dt) {
+            dvacc[dt] = mfma_f16(cv0[0][dt], pk00, dvacc[dt]);
+            dvacc[dt] = mfma_f16(cv0[1][dt], pk01, dvacc[dt]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DQK / 32; ++dt) {
+            dkacc[dt] = mfma_f16(cq0[0][dt], ds00, dkacc[dt]);
+            dkacc[dt] = mfma_f16(cq0[1][dt], ds01, dkacc[dt]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt) cv1[j][dt] = lds_tr<LO>(aO0, aO1, dt, 32 + 16 * j);
+#pragma unroll
+            for (int dt = 0; dt < DQK / 32; ++dt) cq1[j][dt] = lds_tr<LQ>(aQ0, aQ1, dt, 32 + 16 * j);
+        }
+        half8 pk10, pk11, ds10, ds11;
+        elem.template operator()<false>(s1, d1, f1s, f1d, q0 + 32, pk10, pk11, ds10, ds11);
+        asm volatile("" ::"v"(pk10), "v"(pk11), "v"(ds10), "v"(ds11));
+#pragma unroll
+        for (int i = 0; i < NK + NV; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- R4
+#pragma unroll
+        for (int dt = 0; dt < DV / 32; ++dt) {
+            dvacc[dt] = mfma_f16(cv1[0][dt], pk10, dvacc[dt]);
+            dvacc[dt] = mfma_f16(cv1[1][dt], pk11, dvacc[dt]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DQK / 32; ++dt) {
+            dkacc[dt] = mfma_f16(cq1[0][dt], ds10, dkacc[dt]);
+            dkacc[dt] = mfma_f16(cq1[1][dt], ds11, dkacc[dt]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
 
+    // One 32-query sub-tile that needs the causal mask (or lies past it),
+    // computed without pipelining: qs = first query, t = 0 / 1 within the step.
+    auto masked_sub = [&](uint32_t qbase, int t, int qs, bool part) {
+        const uint32_t obase = qbase + Cfg::QB;
+        const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
+        const uint32_t aQ = qbase + swQ.row, aO = obase + swO.row;
+        const uint32_t aQ0 = qbase + swQ.tr0, aQ1 = qbase + swQ.tr1;
+        const uint32_t aO0 = obase + swO.tr0, aO1 = obase + swO.tr1;
+        floatx16 sacc = floatx16{}, dpacc = floatx16{};
+#pragma unroll
+        for (int ks = 0; ks < NK; ++ks) sacc = mfma_f16(lds_row<LQ>(aQ, ks, 32 * t), kreg[ks], sacc);
+#pragma unroll
+        for (int ks = 0; ks < NV; ++ks) dpacc = mfma_f16(lds_row<LO>(aO, ks, 32 * t), vreg[ks], dpacc);
+        floatx4 fs[4], fd[4];
+        read_f(Fs, t, fs, fd);
+        half8 pk0, pk1, ds0, ds1;
+        if (part) elem.template operator()<true>(sacc, dpacc, fs, fd, qs, pk0, pk1, ds0, ds1);
+        else elem.template operator()<false>(sacc, dpacc, fs, fd, qs, pk0, pk1, ds0, ds1);
+#pragma unroll
+        for (int dt = 0; dt < DV / 32; ++dt) {
+            dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t), pk0, dvacc[dt]);
+            dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t + 16), pk1, dvacc[dt]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DQK / 32; ++dt) {
+            dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t), ds0, dkacc[dt]);
+            dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t + 16), ds1, dkacc[dt]);
+        }
+    };
+
+    // Steps whose 64 queries all see all 32 keys of the wave come first
+    // (top-down walk); the causal diagonal and the blocks below it follow.
+    // (Only the one-wave-per-SIMD shape has the registers for the pipeline;
+    // the others run every step through the simple sub-tile path.)
+    const int n_full = Cfg::WAVES != 1 || kw0 >= S_kv ? 0
+                       : !CAUSAL                      ? nsteps
+                                   : (q_top >= kw0 + 32 ? min(nsteps, (q_top - kw0 - 32) / BQ + 1) : 0);
+    int step = 0;
+    if constexpr (Cfg::WAVES == 1) {
+        for (; step < n_full; ++step) {
+            sync_step(step);
+            full_step((uint32_t)((step % NSTAGE) * Cfg::STAGE), q_top - step * BQ);
+        }
+    }
+    for (; step < nsteps; ++step) {
+        sync_step(step);
+        if (kw0 >= S_kv) continue;
+        const int q0 = q_top - step * BQ;
+        const uint32_t qbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int qs = q0 + 32 * t;
             if (qs >= S_q || (CAUSAL && qs + 31 < kw0)) continue;
-            const bool part = CAUSAL && qs < kw0 + 31;
-
-            floatx16 sacc = floatx16{}, dpacc = floatx16{};
-#pragma unroll
-            for (int ks = 0; ks < DQK / 16; ++ks)
-                sacc = mfma_f16(lds_row<LQ>(aQ, ks, 32 * t), kreg[ks], sacc);
-#pragma unroll
-            for (int ks = 0; ks < DV / 16; ++ks)
-                dpacc = mfma_f16(lds_row<LO>(aO, ks, 32 * t), vreg[ks], dpacc);
-            // keep at most two operand reads ahead of the MFMAs
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-            for (int i = 0; i < (DQK + DV) / 16 - 2; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            // rows of the accumulators are queries qs + 8 g + 4 hh + e
-            const uint64_t st_sub = DROP ? st_lane + (uint64_t)qs * row_step : 0;
-            uint32_t wp[8], wd[8];
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int rb = 32 * t + 8 * g + 4 * hh;
-                const floatx4 st4 = *reinterpret_cast<const floatx4*>(Fs + rb);
-                const floatx4 de4 = *reinterpret_cast<const floatx4*>(Fs + BQ + rb);
-                float pk4[4], ds4[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * g + e;
-                    float x = __builtin_fmaf(sacc[r], sl2, -st4[e]);
-                    if (part && my_k > qs + 8 * g + 4 * hh + e) x = -INFINITY;
-                    const float pr = fast_exp2(x);
-                    const bool big = pr > kEps;
-                    float pk, tt;
-                    if constexpr (DROP) {
-                        const bool keep = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr);
-                        pk = (big && keep) ? pr : 0.f;
-                        tt = keep ? __builtin_fmaf(dpacc[r], ksc, -de4[e]) : -de4[e];
-                    } else {
-                        pk = big ? pr : 0.f;
-                        tt = dpacc[r] - de4[e];
-                    }
-                    pk4[e] = pk;
-                    ds4[e] = big ? pr * tt : 0.f;
-                }
-                wp[2 * g] = pack_h2(pk4[0], pk4[1]);
-                wp[2 * g + 1] = pack_h2(pk4[2], pk4[3]);
-                wd[2 * g] = pack_h2(ds4[0], ds4[1]);
-                wd[2 * g + 1] = pack_h2(ds4[2], ds4[3]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            const half8 pkb0 = half8_of(wp[0], wp[1], wp[2], wp[3]);
-            const half8 pkb1 = half8_of(wp[4], wp[5], wp[6], wp[7]);
-            const half8 dsb0 = half8_of(wd[0], wd[1], wd[2], wd[3]);
-            const half8 dsb1 = half8_of(wd[4], wd[5], wd[6], wd[7]);
-#pragma unroll
-            for (int dt = 0; dt < DV / 32; ++dt) {
-                dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t), pkb0, dvacc[dt]);
-                dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t + 16), pkb1, dvacc[dt]);
-            }
-#pragma unroll
-            for (int dt = 0; dt < DQK / 32; ++dt) {
-                dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t), dsb0, dkacc[dt]);
-                dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t + 16), dsb1, dkacc[dt]);
-            }
-            // each MFMA takes two transposed reads; keep two MFMAs' worth ahead
-            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-            for (int i = 0; i < (DQK + DV) / 16 - 2; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            __builtin_amdgcn_sched_barrier(0);
+            masked_sub(qbase, t, qs, CAUSAL && qs < kw0 + 31);
         }
     }
 
