@@ -354,12 +354,12 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         m_run = m_use;
     };
 
-    // One step = 64 keys as two 32-key sub-tiles, software-pipelined so that
-    // every MFMA group has independent work interleaved with it (a wave
-    // issues in order: VALU work placed after a run of MFMAs waits for them):
-    //   R1  S(0) = K0 Q^T           || LDS reads of K1
-    //   R2  S(1) = K1 Q^T           || softmax(0), LDS reads of V0^T
-    //   R3  O^T += V0^T P0~^T       || softmax(1), LDS reads of V1^T
+    // One step = 64 keys as two 32-key sub-tiles, written in software-pipeline
+    // order so that each MFMA group has independent work next to it (a wave
+    // issues in order; the compiler interleaves within these spans):
+    //   R1  S(0) = K0 Q^T           with LDS reads of K1
+    //   R2  S(1) = K1 Q^T           with softmax(0), LDS reads of V0^T
+    //   R3  O^T += V0^T P0~^T       with softmax(1), LDS reads of V1^T
     //   R4  O^T += V1^T P1~^T
     // The rescale of O by sub-tile 1's new maximum commutes with the pending
     // PV(0) accumulation, so it is applied after R3.
@@ -370,7 +370,6 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         half8 ak0[DQK / 16], ak1[DQK / 16];
 #pragma unroll
         for (int ks = 0; ks < DQK / 16; ++ks) ak0[ks] = lds_row<LK>(aK, ks, 0);
-        __builtin_amdgcn_sched_barrier(0);
         // R1
         floatx16 s0 = floatx16{}, s1 = floatx16{};
 #pragma unroll
@@ -378,7 +377,6 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
             s0 = mfma_f16(ak0[ks], qreg[ks], s0);
             ak1[ks] = lds_row<LK>(aK, ks, 32);
         }
-        __builtin_amdgcn_sched_barrier(0);
         // R2
 #pragma unroll
         for (int ks = 0; ks < DQK / 16; ++ks) s1 = mfma_f16(ak1[ks], qreg[ks], s1);
@@ -391,20 +389,7 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         float mu0, al0, ls0;
         half8 p00, p01;
         softmax_sub(s0, 0, st_blk, mu0, al0, ls0, p00, p01);
-        // pin sub-tile 0's softmax inside R2 (its results are used only after
-        // the rescale branch, which would otherwise let them sink below it)
-        asm volatile("" ::"v"(p00), "v"(p01), "v"(ls0), "v"(mu0), "v"(al0));
-        if constexpr (!PART) {
-#pragma unroll
-            for (int i = 0; i < DQK / 16; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 2 * (2 * DV / 32) / (DQK / 16) > 0 ? 2 * (2 * DV / 32) / (DQK / 16) : 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
         commit_sub(mu0, al0, ls0);
-        __builtin_amdgcn_sched_barrier(0);
         // R3
 #pragma unroll
         for (int dt = 0; dt < DV / 32; ++dt) {
@@ -419,18 +404,7 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         float mu1, al1, ls1;
         half8 p10, p11;
         softmax_sub(s1, 1, st_blk, mu1, al1, ls1, p10, p11);
-        asm volatile("" ::"v"(p10), "v"(p11), "v"(ls1), "v"(mu1), "v"(al1));
-        if constexpr (!PART) {
-#pragma unroll
-            for (int i = 0; i < 2 * DV / 32; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 14, 0);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
         commit_sub(mu1, al1, ls1);
-        __builtin_amdgcn_sched_barrier(0);
         // R4
 #pragma unroll
         for (int dt = 0; dt < DV / 32; ++dt) {
@@ -702,12 +676,20 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     for (int i = 0; i < NSTAGE - 1; ++i)
         if (i < nsteps) issue(i);
     // Wait for block `step` (the copies of the NSTAGE - 2 later blocks may
-    // still fly; all of them at the tail), synchronise, start the next copy.
+    // still fly; all of them at the tail) and synchronise.  The copy of block
+    // step + NSTAGE - 1 goes out at the end of the step (`next_copy`), where
+    // its issue stall overlaps the wave's wait at the following barrier; its
+    // stage held block step - 1, which every wave finished before this
+    // step's barrier (NSTAGE >= 3 keeps one step of prefetch).
+    static_assert(NSTAGE >= 3 || Cfg::WAVES != 1, "end-of-step copies need a third stage");
     auto sync_step = [&](int step) {
         if (step + NSTAGE - 2 < nsteps) wait_vm_n<(NSTAGE - 2) * LPS>();
         else wait_vm();
         __syncthreads();
-        if (step + NSTAGE - 1 < nsteps) issue(step + NSTAGE - 1);
+        if (NSTAGE < 3 && step + NSTAGE - 1 < nsteps) issue(step + NSTAGE - 1);
+    };
+    auto next_copy = [&](int step) {
+        if (NSTAGE >= 3 && step + NSTAGE - 1 < nsteps) issue(step + NSTAGE - 1);
     };
 
     const float sl2 = p.c.scale_log2;
@@ -773,9 +755,9 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     };
 
     // One step of 64 queries whose two 32-query sub-tiles are fully visible
-    // to the wave's keys, software-pipelined (a wave issues in order, so the
-    // element-wise work of one sub-tile is interleaved with the MFMAs of
-    // another):
+    // to the wave's keys, written in software-pipeline order (a wave issues
+    // in order, so the element-wise work of one sub-tile is placed next to
+    // the MFMAs of another; the compiler interleaves within each span):
     //   R1  A(0): S, dP of sub-tile 0           || reads of A(1) operands, F(0)
     //   R2  A(1)                                 || B(0) elementwise, reads of C(0) operands, F(1)
     //   R3  C(0): dV += dO0^T P0~, dK += Q0^T dS0 || B(1), reads of C(1) operands
@@ -793,7 +775,6 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
             if (ks < NK) aq0[ks] = lds_row<LQ>(aQ, ks, 0);
             if (ks < NV) ao0[ks] = lds_row<LO>(aO, ks, 0);
         }
-        __builtin_amdgcn_sched_barrier(0);
         // ---- R1
         floatx16 s0 = floatx16{}, d0 = floatx16{}, s1 = floatx16{}, d1 = floatx16{};
 #pragma unroll
@@ -808,12 +789,6 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
         }
         floatx4 f0s[4], f0d[4], f1s[4], f1d[4];
         read_f(Fs, 0, f0s, f0d);
-#pragma unroll
-        for (int i = 0; i < NK + NV; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
         // ---- R2
 #pragma unroll
         for (int ks = 0; ks < NA; ++ks) {
@@ -831,14 +806,6 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
         read_f(Fs, 1, f1s, f1d);
         half8 pk00, pk01, ds00, ds01;
         elem.template operator()<false>(s0, d0, f0s, f0d, q0, pk00, pk01, ds00, ds01);
-        asm volatile("" ::"v"(pk00), "v"(pk01), "v"(ds00), "v"(ds01));
-#pragma unroll
-        for (int i = 0; i < NK + NV; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
         // ---- R3
 #pragma unroll
         for (int dt = 0; dt < DV / 32; ++dt) {
@@ -859,14 +826,6 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
         }
         half8 pk10, pk11, ds10, ds11;
         elem.template operator()<false>(s1, d1, f1s, f1d, q0 + 32, pk10, pk11, ds10, ds11);
-        asm volatile("" ::"v"(pk10), "v"(pk11), "v"(ds10), "v"(ds11));
-#pragma unroll
-        for (int i = 0; i < NK + NV; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
         // ---- R4
 #pragma unroll
         for (int dt = 0; dt < DV / 32; ++dt) {
@@ -878,7 +837,6 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
             dkacc[dt] = mfma_f16(cq1[0][dt], ds10, dkacc[dt]);
             dkacc[dt] = mfma_f16(cq1[1][dt], ds11, dkacc[dt]);
         }
-        __builtin_amdgcn_sched_barrier(0);
     };
 
     // One 32-query sub-tile that needs the causal mask (or lies past it),
@@ -923,19 +881,22 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
         for (; step < n_full; ++step) {
             sync_step(step);
             full_step((uint32_t)((step % NSTAGE) * Cfg::STAGE), q_top - step * BQ);
+            next_copy(step);
         }
     }
     for (; step < nsteps; ++step) {
         sync_step(step);
-        if (kw0 >= S_kv) continue;
-        const int q0 = q_top - step * BQ;
-        const uint32_t qbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE);
+        if (kw0 < S_kv) {
+            const int q0 = q_top - step * BQ;
+            const uint32_t qbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int qs = q0 + 32 * t;
-            if (qs >= S_q || (CAUSAL && qs + 31 < kw0)) continue;
-            masked_sub(qbase, t, qs, CAUSAL && qs < kw0 + 31);
+            for (int t = 0; t < 2; ++t) {
+                const int qs = q0 + 32 * t;
+                if (qs >= S_q || (CAUSAL && qs + 31 < kw0)) continue;
+                masked_sub(qbase, t, qs, CAUSAL && qs < kw0 + 31);
+            }
         }
+        next_copy(step);
     }
 
     if (key_ok) {
