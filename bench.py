@@ -223,8 +223,10 @@ def main():
     achieved = kflops[dom] / (per[dom] * 1e-3) / 1e12
     # fp16 shapes with D % 8 == 0 run the DMA-fed kernels (sdpa_f16_dma.hip)
     sfx = "f16_dma" if (dt == "f16" and D_qk % 8 == 0 and D_v % 8 == 0) else dt
+    # (dK/dV of a feature width above 64 runs the split-role variant)
+    kv_sfx = "f16_split" if (sfx == "f16_dma" and max(D_qk, D_v) > 64) else sfx
     kernel_symbol = {"sdpa_fwd": "sdpa_fwd_%s_kernel" % sfx, "sdpa_bwd_dq": "sdpa_bwd_dq_%s_kernel" % sfx,
-                     "sdpa_bwd_dkdv": "sdpa_bwd_dkdv_%s_kernel" % sfx}[dom]
+                     "sdpa_bwd_dkdv": "sdpa_bwd_dkdv_%s_kernel" % kv_sfx}[dom]
 
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * (1 << 20)

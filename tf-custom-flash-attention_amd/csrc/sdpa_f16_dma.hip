@@ -604,6 +604,12 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
 // ===========================================================================
 // Backward, dK/dV kernel (reads stats2 and delta from the workspace)
 // ===========================================================================
+// Shapes with a 128-wide side run the split-role kernel further below unless
+// this is 0.
+#ifndef SDPA_DKDV_SPLIT
+#define SDPA_DKDV_SPLIT 1
+#endif
+
 template <int DQK, int DV>
 struct DkvDmaCfg {
     static constexpr int NT = 256, BKV = 128, BQ = 64;
@@ -909,6 +915,269 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     }
 }
 
+// ===========================================================================
+// Backward, dK/dV kernel with the work of a key split over two waves
+// ===========================================================================
+// Eight waves over 128 keys.  Waves w and w + 4 (w < 4) own keys
+// k0 + 32 w .. + 31 and run on the same SIMD:
+//   wave w      (P role):  S = Q K^T, P = exp2(S sl2 - stats2), P~ = P * keep,
+//                          dV^T += dO^T P~; it hands P to wave w + 4 through
+//                          LDS with the dropout decision in the sign (-P for a
+//                          dropped element);
+//   wave w + 4  (dS role): dP = dO V^T, dS = P (keep ? dP ksc - delta : -delta),
+//                          dK^T += Q^T dS, one block behind the P role.
+// Each role holds one operand (K or V, 32 VGPRs) and one accumulator (64), so
+// both roles fit two waves per SIMD, and every SIMD still does the four GEMMs
+// of its 32 keys once per block.  The dS role also copies the tiles.
+//
+// LDS: a ring of three blocks (Q, dO, stats2, delta) and two P exchange
+// buffers.  During step n the P role reads block n, the dS role reads block
+// n - 1 and P of step n - 1, and the copy of block n + 1 is in flight; it was
+// issued after the barrier that opened step n, into the ring slot of block
+// n - 2.
+template <int DQK, int DV>
+struct DkvSplitCfg {
+    static constexpr int NT = 512, BKV = 128, BQ = 64, NSTAGE = 3;
+    static constexpr int LQ = DQK / 8, LO = DV / 8;
+    static constexpr int QB = BQ * DQK * 2, OB = BQ * DV * 2, FB = 2 * BQ * 4;
+    static constexpr int STAGE = QB + OB + FB;
+    // P of one block: 4 key groups x 2 sub-tiles x 64 lanes x 16 halves
+    static constexpr int XB = 4 * 2 * 64 * 32;
+    static constexpr size_t LDS_BYTES = NSTAGE * (size_t)STAGE + 2 * XB;
+    static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS");
+};
+
+template <int DQK, int DV, bool CAUSAL, bool DROP>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
+    using Cfg = DkvSplitCfg<DQK, DV>;
+    constexpr int BKV = Cfg::BKV, BQ = Cfg::BQ, LQ = Cfg::LQ, LO = Cfg::LO, NSTAGE = Cfg::NSTAGE;
+
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kw = wave & 3;
+    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
+    const int tiles = (S_kv + BKV - 1) / BKV;
+    int b, kt;
+    xcd_map(blockIdx.x, B * tiles, tiles, false, b, kt);
+    const int k0 = kt * BKV, kw0 = k0 + 32 * kw, my_k = kw0 + l32;
+    const bool key_ok = my_k < S_kv;
+
+    const half_t* Qb = static_cast<const half_t*>(p.q) + (size_t)b * S_q * D_qk;
+    const half_t* dOb = static_cast<const half_t*>(p.d_o) + (size_t)b * S_q * D_v;
+
+    // Query blocks walked top-down (see the one-wave kernel above).
+    const int q_begin = CAUSAL ? (min(k0, S_q) / BQ) * BQ : 0;
+    const int nsteps = (S_q - q_begin + BQ - 1) / BQ;
+    const int q_top = q_begin + (nsteps - 1) * BQ;
+
+    // Sub-tile t of block m: queries qs = q0 + 32 t; skipped (by both roles)
+    // when past S_q, past the keys or, under the causal mask, above every key.
+    auto sub_live = [&](int qs) {
+        return kw0 < S_kv && qs < S_q && !(CAUSAL && qs + 31 < kw0);
+    };
+    auto xbuf = [&](int m, int t) {
+        return smem + NSTAGE * Cfg::STAGE + (m & 1) * Cfg::XB + (kw * 2 + t) * 2048 + lane * 16;
+    };
+
+    if (wave < 4) {
+        // ------------------------------------------------------------ P role
+        half8 kreg[DQK / 16];
+        const half_t* Kb = static_cast<const half_t*>(p.k) + (size_t)b * S_kv * D_qk;
+#pragma unroll
+        for (int ks = 0; ks < DQK / 16; ++ks)
+            kreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Kb, my_k, S_kv, 16 * ks + 8 * hh, D_qk, D_qk));
+        const float sl2 = p.c.scale_log2;
+        // Dropout: st(q, key) = st(4 hh, key) + q * S_kv * A.
+        const uint64_t st_lane = DROP ? lcg_state(p.c.seed_offset, (uint64_t)b * S_q + 4 * hh, (uint64_t)S_kv, my_k) : 0;
+        const uint64_t row_step = (uint64_t)S_kv * kLcgMul;
+        const uint32_t thr = p.c.drop_threshold;
+        SwzLane<LQ> swQ;
+        SwzLane<LO> swO;
+        swQ.init(lane);
+        swO.init(lane);
+        floatx16 dvacc[DV / 32];
+#pragma unroll
+        for (int dt = 0; dt < DV / 32; ++dt) dvacc[dt] = floatx16{};
+
+        // P of one sub-tile: pk = P~ as the dV B operand, xv = P with the
+        // dropout decision in the sign, for the dS role.
+        auto elem = [&]<bool MASK>(const floatx16& sacc, const floatx4 (&st4)[4], int qs, half8& pk0, half8& pk1,
+                                   half8& xv0, half8& xv1) {
+            uint64_t st_sub = DROP ? st_lane + (uint64_t)qs * row_step : 0;
+            // Hash states after S: computed all at once above the MFMAs they
+            // would hold 32 VGPRs through the chain.
+            if constexpr (DROP) asm volatile("" : "+v"(st_sub) : "v"(sacc[15]));
+            uint32_t wp[8], wx[8];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float pk4[4], x4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float x = __builtin_fmaf(sacc[4 * g + e], sl2, -st4[g][e]);
+                    if (MASK && my_k > qs + 8 * g + 4 * hh + e) x = -INFINITY;
+                    float pr = fast_exp2(x);
+                    pr = pr > kEps ? pr : 0.f;
+                    if constexpr (DROP) {
+                        const bool keep = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr);
+                        pk4[e] = keep ? pr : 0.f;
+                        x4[e] = keep ? pr : -pr;
+                    } else {
+                        pk4[e] = pr;
+                        x4[e] = pr;
+                    }
+                }
+                wp[2 * g] = pack_h2(pk4[0], pk4[1]);
+                wp[2 * g + 1] = pack_h2(pk4[2], pk4[3]);
+                if constexpr (DROP) {
+                    wx[2 * g] = pack_h2(x4[0], x4[1]);
+                    wx[2 * g + 1] = pack_h2(x4[2], x4[3]);
+                }
+            }
+            pk0 = half8_of(wp[0], wp[1], wp[2], wp[3]);
+            pk1 = half8_of(wp[4], wp[5], wp[6], wp[7]);
+            if constexpr (DROP) {
+                xv0 = half8_of(wx[0], wx[1], wx[2], wx[3]);
+                xv1 = half8_of(wx[4], wx[5], wx[6], wx[7]);
+            } else {
+                xv0 = pk0;
+                xv1 = pk1;
+            }
+        };
+        auto sub = [&]<bool MASK>(uint32_t qbase, int m, int t, int qs) {
+            const uint32_t obase = qbase + Cfg::QB;
+            const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
+            const uint32_t aQ = qbase + swQ.row;
+            const uint32_t aO0 = obase + swO.tr0, aO1 = obase + swO.tr1;
+            floatx16 sacc = floatx16{};
+#pragma unroll
+            for (int ks = 0; ks < DQK / 16; ++ks) sacc = mfma_f16(lds_row<LQ>(aQ, ks, 32 * t), kreg[ks], sacc);
+            floatx4 st4[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) st4[g] = *reinterpret_cast<const floatx4*>(Fs + 32 * t + 8 * g + 4 * hh);
+            half8 pk0, pk1, xv0, xv1;
+            elem.template operator()<MASK>(sacc, st4, qs, pk0, pk1, xv0, xv1);
+            unsigned char* xs = xbuf(m, t);
+            *reinterpret_cast<half8*>(xs) = xv0;
+            *reinterpret_cast<half8*>(xs + 1024) = xv1;
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt) {
+                dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t), pk0, dvacc[dt]);
+                dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t + 16), pk1, dvacc[dt]);
+            }
+        };
+        // nsteps + 1 barriers, as many as the dS role.
+        for (int n = 0; n <= nsteps; ++n) {
+            __syncthreads();
+            if (n == nsteps) break;
+            const int q0 = q_top - n * BQ;
+            const uint32_t qbase = (uint32_t)((n % NSTAGE) * Cfg::STAGE);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int qs = q0 + 32 * t;
+                if (!sub_live(qs)) continue;
+                if (CAUSAL && qs < kw0 + 31) sub.template operator()<true>(qbase, n, t, qs);
+                else sub.template operator()<false>(qbase, n, t, qs);
+            }
+        }
+        if (key_ok) {
+            half_t* dVb = static_cast<half_t*>(p.dv) + ((size_t)b * S_kv + my_k) * D_v;
+            if (D_v == DV) store_rows_f16<DV>(dVb, dvacc, p.c.keep_scale, hh);
+            else store_rows_f16_n<DV>(dVb, dvacc, p.c.keep_scale, hh, D_v);
+        }
+    } else {
+        // ----------------------------------------------------------- dS role
+        half8 vreg[DV / 16];
+        const half_t* Vb = static_cast<const half_t*>(p.v) + (size_t)b * S_kv * D_v;
+#pragma unroll
+        for (int ks = 0; ks < DV / 16; ++ks)
+            vreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Vb, my_k, S_kv, 16 * ks + 8 * hh, D_v, D_v));
+        const float* st2b = p.stats2 + (size_t)b * S_q;
+        const float* deltab = p.delta + (size_t)b * S_q;
+        TileDma<BQ, LQ, 4> qd;
+        TileDma<BQ, LO, 4> od;
+        constexpr int LPS = TileDma<BQ, LQ, 4>::MIN_PER_WAVE + TileDma<BQ, LO, 4>::MIN_PER_WAVE;
+        qd.init(kw, lane, D_qk * 2, D_qk / 8);
+        od.init(kw, lane, D_v * 2, D_v / 8);
+        auto issue = [&](int m) {
+            const int q0 = q_top - m * BQ;
+            unsigned char* st = smem + (m % NSTAGE) * Cfg::STAGE;
+            qd.issue(make_rsrc(Qb + (size_t)q0 * D_qk, (long long)(S_q - q0) * D_qk * 2), st, kw);
+            od.issue(make_rsrc(dOb + (size_t)q0 * D_v, (long long)(S_q - q0) * D_v * 2), st + Cfg::QB, kw);
+            if (kw == 0) dma4(make_rsrc(st2b + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB, lane * 4);
+            if (kw == 1) dma4(make_rsrc(deltab + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB + BQ * 4, lane * 4);
+        };
+        if (nsteps > 0) issue(0);
+        if (nsteps > 1) issue(1);
+        const float ksc = p.c.keep_scale;
+        SwzLane<LQ> swQ;
+        SwzLane<LO> swO;
+        swQ.init(lane);
+        swO.init(lane);
+        floatx16 dkacc[DQK / 32];
+#pragma unroll
+        for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};
+
+        auto sub = [&](uint32_t qbase, int m, int t) {
+            const uint32_t obase = qbase + Cfg::QB;
+            const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
+            const uint32_t aO = obase + swO.row;
+            const uint32_t aQ0 = qbase + swQ.tr0, aQ1 = qbase + swQ.tr1;
+            floatx16 dpacc = floatx16{};
+#pragma unroll
+            for (int ks = 0; ks < DV / 16; ++ks) dpacc = mfma_f16(lds_row<LO>(aO, ks, 32 * t), vreg[ks], dpacc);
+            floatx4 de4[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) de4[g] = *reinterpret_cast<const floatx4*>(Fs + BQ + 32 * t + 8 * g + 4 * hh);
+            const unsigned char* xs = xbuf(m, t);
+            const half8 xv0 = *reinterpret_cast<const half8*>(xs);
+            const half8 xv1 = *reinterpret_cast<const half8*>(xs + 1024);
+            uint32_t wd[8];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float ds4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * g + e;
+                    const float xq = (float)(r < 8 ? xv0[r] : xv1[r - 8]);
+                    if constexpr (DROP)
+                        ds4[e] = __builtin_fmaf(fmaxf(xq, 0.f), dpacc[r] * ksc, -__builtin_fabsf(xq) * de4[g][e]);
+                    else
+                        ds4[e] = xq * (dpacc[r] - de4[g][e]);
+                }
+                wd[2 * g] = pack_h2(ds4[0], ds4[1]);
+                wd[2 * g + 1] = pack_h2(ds4[2], ds4[3]);
+            }
+            const half8 ds0 = half8_of(wd[0], wd[1], wd[2], wd[3]);
+            const half8 ds1 = half8_of(wd[4], wd[5], wd[6], wd[7]);
+#pragma unroll
+            for (int dt = 0; dt < DQK / 32; ++dt) {
+                dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t), ds0, dkacc[dt]);
+                dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t + 16), ds1, dkacc[dt]);
+            }
+        };
+        for (int n = 0; n <= nsteps; ++n) {
+            // block n has landed (block 1 may still fly at n = 0)
+            if (n == 0 && nsteps > 1) wait_vm_n<LPS>();
+            else wait_vm();
+            __syncthreads();
+            if (n >= 1 && n + 1 < nsteps) issue(n + 1);
+            if (n == 0) continue;
+            const int m = n - 1;
+            const int q0 = q_top - m * BQ;
+            const uint32_t qbase = (uint32_t)((m % NSTAGE) * Cfg::STAGE);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                if (sub_live(q0 + 32 * t)) sub(qbase, m, t);
+        }
+        if (key_ok) {
+            half_t* dKb = static_cast<half_t*>(p.dk) + ((size_t)b * S_kv + my_k) * D_qk;
+            if (D_qk == DQK) store_rows_f16<DQK>(dKb, dkacc, p.c.scale, hh);
+            else store_rows_f16_n<DQK>(dKb, dkacc, p.c.scale, hh, D_qk);
+        }
+    }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -950,9 +1219,16 @@ hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream
                                                                                    CQ::LDS_BYTES, stream, p);
                     }
                     if (err == hipSuccess && (phases & kBwdDkDv) && S_kv > 0) {
-                        const long long n = (long long)((S_kv + CK::BKV - 1) / CK::BKV) * B;
-                        err = launch_kernel<sdpa_bwd_dkdv_f16_dma_kernel<DQK, DV, CA, DR>>((unsigned)n, CK::NT,
-                                                                                     CK::LDS_BYTES, stream, p);
+                        if constexpr (CK::WAVES == 1 && SDPA_DKDV_SPLIT) {
+                            using CS = DkvSplitCfg<DQK, DV>;
+                            const long long n = (long long)((S_kv + CS::BKV - 1) / CS::BKV) * B;
+                            err = launch_kernel<sdpa_bwd_dkdv_f16_split_kernel<DQK, DV, CA, DR>>(
+                                (unsigned)n, CS::NT, CS::LDS_BYTES, stream, p);
+                        } else {
+                            const long long n = (long long)((S_kv + CK::BKV - 1) / CK::BKV) * B;
+                            err = launch_kernel<sdpa_bwd_dkdv_f16_dma_kernel<DQK, DV, CA, DR>>(
+                                (unsigned)n, CK::NT, CK::LDS_BYTES, stream, p);
+                        }
                     }
                     return err;
                 });
