@@ -43,27 +43,55 @@
 namespace sdpa {
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Buffer descriptor (four SGPRs): base address, stride 0, num_records, and
+// the word-3 configuration of a raw buffer on gfx950.
+typedef int rsrc_t __attribute__((ext_vector_type(4)));
 
 // A voffset at or past num_records: the load returns zero and touches nothing.
 constexpr uint32_t kOob = 0x80000000u;
 // Lazy-rescale threshold of the forward's running maximum (log2 units).
 constexpr float kTauF = 8.0f;
 
-// Raw buffer descriptor over [base, base + bytes).
+extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+
+// Raw buffer descriptor over [base, base + bytes); every field is wave-uniform.
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, long long bytes) {
     const int n = bytes <= 0 ? 0 : (bytes >= 0x7FFFFFFFLL ? 0x7FFFFFFF : (int)bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return (rsrc_t){__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                    __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu)),
+                    __builtin_amdgcn_readfirstlane(n), 0x00020000};
 }
 
-// 16 (or 4) bytes per lane from byte offset voff into LDS at wave_dst + 16 L (4 L).
+// LDS byte address of a pointer into smem.
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(base + (uint32_t)(p - smem)));
+}
+
+// 16 (or 4) bytes per lane from byte offset voff into LDS at wave_dst + 16 L
+// (4 L).  The copies are issued from inline assembly: the compiler does not
+// track them, so it adds no vmcnt waits of its own in front of later LDS
+// reads (with the builtin it waits for every copy in flight before each
+// ds_read_b64_tr_b16).  The kernels order copies and reads themselves: a
+// stage is read only after wait_vm / wait_vm_n and a barrier, and a copy
+// into a stage is issued only after a barrier that follows its last read.
+// M0 holds the LDS base of the copy; the s_nop covers the M0 -> LDS-DMA hazard.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* wave_dst, uint32_t voff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)wave_dst, 16, voff, 0, 0, 0);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr(wave_dst)), "v"(voff), "s"(r)
+                 : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(rsrc_t r, unsigned char* wave_dst, uint32_t voff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)wave_dst, 4, voff, 0, 0, 0);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr(wave_dst)), "v"(voff), "s"(r)
+                 : "memory", "m0");
 }
+#pragma clang diagnostic pop
 // s_waitcnt vmcnt(0): this wave's copies (and loads) have landed.
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -158,7 +186,12 @@ struct SwzLane {
     }
 };
 
-extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
+// max(x, 0) of eight finite halves as a signed 16-bit max on their bit
+// patterns (a set sign bit is a negative int16), one v_pk_max_i16 per pair.
+__device__ __forceinline__ half8 relu_h8(half8 x) {
+    typedef short short8 __attribute__((ext_vector_type(8)));
+    return __builtin_bit_cast(half8, __builtin_elementwise_max(__builtin_bit_cast(short8, x), short8{}));
+}
 
 // Row-read A operand: rows R0 + l32 (R0 % 16 == 0), k-step ks.
 // `a` = tile base + SwzLane::row.
@@ -1000,48 +1033,40 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
         for (int dt = 0; dt < DV / 32; ++dt) dvacc[dt] = floatx16{};
 
-        // P of one sub-tile: pk = P~ as the dV B operand, xv = P with the
-        // dropout decision in the sign, for the dS role.
+        // P of one sub-tile: xv = P with the dropout decision in the sign (for
+        // the dS role), pk = max(xv, 0) = P~ (the dV B operand).
         auto elem = [&]<bool MASK>(const floatx16& sacc, const floatx4 (&st4)[4], int qs, half8& pk0, half8& pk1,
                                    half8& xv0, half8& xv1) {
             uint64_t st_sub = DROP ? st_lane + (uint64_t)qs * row_step : 0;
             // Hash states after S: computed all at once above the MFMAs they
             // would hold 32 VGPRs through the chain.
             if constexpr (DROP) asm volatile("" : "+v"(st_sub) : "v"(sacc[15]));
-            uint32_t wp[8], wx[8];
+            uint32_t wx[8];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                float pk4[4], x4[4];
+                float x4[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float x = __builtin_fmaf(sacc[4 * g + e], sl2, -st4[g][e]);
                     if (MASK && my_k > qs + 8 * g + 4 * hh + e) x = -INFINITY;
-                    float pr = fast_exp2(x);
-                    pr = pr > kEps ? pr : 0.f;
-                    if constexpr (DROP) {
-                        const bool keep = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr);
-                        pk4[e] = keep ? pr : 0.f;
-                        x4[e] = keep ? pr : -pr;
-                    } else {
-                        pk4[e] = pr;
-                        x4[e] = pr;
-                    }
+                    const float pr = fast_exp2(x);
+                    const float pe = pr > kEps ? pr : 0.f;
+                    if constexpr (DROP)
+                        x4[e] = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr) ? pe : -pe;
+                    else
+                        x4[e] = pe;
                 }
-                wp[2 * g] = pack_h2(pk4[0], pk4[1]);
-                wp[2 * g + 1] = pack_h2(pk4[2], pk4[3]);
-                if constexpr (DROP) {
-                    wx[2 * g] = pack_h2(x4[0], x4[1]);
-                    wx[2 * g + 1] = pack_h2(x4[2], x4[3]);
-                }
+                wx[2 * g] = pack_h2(x4[0], x4[1]);
+                wx[2 * g + 1] = pack_h2(x4[2], x4[3]);
             }
-            pk0 = half8_of(wp[0], wp[1], wp[2], wp[3]);
-            pk1 = half8_of(wp[4], wp[5], wp[6], wp[7]);
+            xv0 = half8_of(wx[0], wx[1], wx[2], wx[3]);
+            xv1 = half8_of(wx[4], wx[5], wx[6], wx[7]);
             if constexpr (DROP) {
-                xv0 = half8_of(wx[0], wx[1], wx[2], wx[3]);
-                xv1 = half8_of(wx[4], wx[5], wx[6], wx[7]);
+                pk0 = relu_h8(xv0);
+                pk1 = relu_h8(xv1);
             } else {
-                xv0 = pk0;
-                xv1 = pk1;
+                pk0 = xv0;
+                pk1 = xv1;
             }
         };
         auto sub = [&]<bool MASK>(uint32_t qbase, int m, int t, int qs) {
@@ -1092,6 +1117,15 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
         for (int ks = 0; ks < DV / 16; ++ks)
             vreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Vb, my_k, S_kv, 16 * ks + 8 * hh, D_v, D_v));
+        // With dropout V is held as V / (1 - p) (rounded to fp16), so the MFMA
+        // yields dP / (1 - p) directly.
+        if constexpr (DROP) {
+            const float ksc = p.c.keep_scale;
+#pragma unroll
+            for (int ks = 0; ks < DV / 16; ++ks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vreg[ks][e] = (half_t)((float)vreg[ks][e] * ksc);
+        }
         const float* st2b = p.stats2 + (size_t)b * S_q;
         const float* deltab = p.delta + (size_t)b * S_q;
         TileDma<BQ, LQ, 4> qd;
@@ -1109,7 +1143,6 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         };
         if (nsteps > 0) issue(0);
         if (nsteps > 1) issue(1);
-        const float ksc = p.c.keep_scale;
         SwzLane<LQ> swQ;
         SwzLane<LO> swO;
         swQ.init(lane);
@@ -1118,6 +1151,32 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
         for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};
 
+        // dS of one sub-tile from dP' (dP / (1 - p)), delta and the P role's x.
+        auto elem = [&](const floatx16& dpacc, const floatx4 (&de4)[4], const half8& xv0, const half8& xv1,
+                        half8& ds0, half8& ds1) {
+            // dS = P (keep ? dP' - delta : -delta) = max(x, 0) dP' - |x| delta
+            const half8 xm0 = DROP ? relu_h8(xv0) : xv0;
+            const half8 xm1 = DROP ? relu_h8(xv1) : xv1;
+            uint32_t wd[8];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float ds4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * g + e;
+                    const float xq = (float)(r < 8 ? xv0[r] : xv1[r - 8]);
+                    const float mq = (float)(r < 8 ? xm0[r] : xm1[r - 8]);
+                    if constexpr (DROP)
+                        ds4[e] = __builtin_fmaf(-__builtin_fabsf(xq), de4[g][e], mq * dpacc[r]);
+                    else
+                        ds4[e] = xq * (dpacc[r] - de4[g][e]);
+                }
+                wd[2 * g] = pack_h2(ds4[0], ds4[1]);
+                wd[2 * g + 1] = pack_h2(ds4[2], ds4[3]);
+            }
+            ds0 = half8_of(wd[0], wd[1], wd[2], wd[3]);
+            ds1 = half8_of(wd[4], wd[5], wd[6], wd[7]);
+        };
         auto sub = [&](uint32_t qbase, int m, int t) {
             const uint32_t obase = qbase + Cfg::QB;
             const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
@@ -1130,26 +1189,8 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) de4[g] = *reinterpret_cast<const floatx4*>(Fs + BQ + 32 * t + 8 * g + 4 * hh);
             const unsigned char* xs = xbuf(m, t);
-            const half8 xv0 = *reinterpret_cast<const half8*>(xs);
-            const half8 xv1 = *reinterpret_cast<const half8*>(xs + 1024);
-            uint32_t wd[8];
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float ds4[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * g + e;
-                    const float xq = (float)(r < 8 ? xv0[r] : xv1[r - 8]);
-                    if constexpr (DROP)
-                        ds4[e] = __builtin_fmaf(fmaxf(xq, 0.f), dpacc[r] * ksc, -__builtin_fabsf(xq) * de4[g][e]);
-                    else
-                        ds4[e] = xq * (dpacc[r] - de4[g][e]);
-                }
-                wd[2 * g] = pack_h2(ds4[0], ds4[1]);
-                wd[2 * g + 1] = pack_h2(ds4[2], ds4[3]);
-            }
-            const half8 ds0 = half8_of(wd[0], wd[1], wd[2], wd[3]);
-            const half8 ds1 = half8_of(wd[4], wd[5], wd[6], wd[7]);
+            half8 ds0, ds1;
+            elem(dpacc, de4, *reinterpret_cast<const half8*>(xs), *reinterpret_cast<const half8*>(xs + 1024), ds0, ds1);
 #pragma unroll
             for (int dt = 0; dt < DQK / 32; ++dt) {
                 dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t), ds0, dkacc[dt]);
