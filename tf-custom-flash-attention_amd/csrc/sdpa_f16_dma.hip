@@ -13,9 +13,9 @@
 // chunk-swizzled layout of swz_off() (conflict-free row and transpose reads)
 // without passing through VGPRs.  The buffer descriptor of every tile starts
 // at the tile's first row and ends at the end of the batch row, so rows past
-// S and columns past D read as zero: tails need no branches.  Two LDS stages:
-// the copy of step n+1 is in flight while step n is multiplied, with one
-// barrier per step.
+// S and columns past D read as zero: tails need no branches.  Forward and dQ
+// use two LDS stages (the copy of step n+1 is in flight while step n is
+// multiplied, one barrier per step); dK/dV uses a ring of three.
 //
 // Work order.  Workgroup ids are remapped so that each XCD (ids are dealt
 // round-robin over the 8 XCDs) walks whole batch rows: all tiles of a batch
@@ -28,8 +28,10 @@
 //     S^T = K Q^T, online softmax over keys, O^T += V^T P~^T
 //   dQ, per wave of 32 queries:
 //     S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T
-//   dK/dV, per wave of 32 keys (lane = key):
+//   dK/dV, per group of 32 keys (lane = key):
 //     S = Q K^T, dP = dO V^T, dV^T += dO^T P~, dK^T += Q^T dS
+//     (one wave per group, or at a 128-wide side two: one for S, P and dV,
+//     one for dP, dS and dK)
 // Element semantics are those of the reference (sdpa/sdpa_fwd.cu.cc:93-173,
 // sdpa/sdpa_bwd.cu.cc:130-170, 291-327), restated in sdpa_fwd.hip and
 // sdpa_bwd.hip.
@@ -95,39 +97,41 @@ __device__ __forceinline__ void dma4(rsrc_t r, unsigned char* wave_dst, uint32_t
 // s_waitcnt vmcnt(0): this wave's copies (and loads) have landed.
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Per-lane global offsets of one ROWS x (8 L) fp16 tile copied by NW waves
-// (NW = 4 or 8).  LDS chunk slot p (16 bytes) of the tile is row p / L,
-// position p % L; it receives global chunk (p % L) ^ swz<L>(row) of that row.
-// Copy u of wave w fills slots (NW u + w) * 64 + lane, i.e. rows
-// (NW u + w) * 64 / L + lane / L; for NW in {4, 8} and every L the swizzle
-// term of those rows does not depend on u, so one offset per lane plus
-// u * NW * 64 / L rows covers all of the wave's copies.
+// Per-lane global offsets of one ROWS x (8 L) fp16 tile copied by NW waves.
+// LDS chunk slot p (16 bytes) of the tile is row p / L, position p % L; it
+// receives global chunk (p % L) ^ swz<L>(row) of that row.  Copy u of wave w
+// fills slots (NW u + w) * 64 + lane, i.e. rows (NW u + w) * 64 / L + lane / L.
+// The swizzle term depends on the row modulo 16, so it repeats every PERIOD
+// copies (PERIOD = 1 when a round of NW copies spans a multiple of 16 rows):
+// PERIOD offsets per lane plus whole rounds of rows cover all of the wave's
+// copies.
 template <int ROWS, int L, int NW>
 struct TileDma {
     static constexpr int LOADS = ROWS * L / 64;  // wave-sized copies per tile
     static constexpr int PER_WAVE = (LOADS + NW - 1) / NW;
     static constexpr int MIN_PER_WAVE = LOADS / NW;  // copies issued by every wave
-    static_assert(NW == 4 || NW == 8, "swizzle term is copy-invariant for 4 or 8 waves");
-    uint32_t voff0;     // offset of copy 0, or kOob for chunks past D
-    uint32_t row_step;  // bytes between consecutive copies of a wave
+    static constexpr int RPR = NW * 64 / L;          // rows per round of NW copies
+    static constexpr int PERIOD = RPR % 16 == 0 ? 1 : 16 / RPR;
+    static_assert(RPR % 16 == 0 || 16 % RPR == 0, "round must divide or be a multiple of 16 rows");
+    uint32_t voff0[PERIOD];  // offsets of copies 0 .. PERIOD-1 (kOob for chunks past D)
+    uint32_t row_step;       // bytes between copies u and u + PERIOD
 
     // row_bytes: global row pitch; valid_chunks: 16-byte chunks inside D.
     __device__ __forceinline__ void init(int wave, int lane, int row_bytes, int valid_chunks) {
-        const int slot = wave * 64 + lane;
-        const int r = slot / L;
-        const int c = (slot % L) ^ swz<L>(r);
-        voff0 = c < valid_chunks ? (uint32_t)(r * row_bytes + c * 16) : kOob;
-        row_step = (uint32_t)((NW * 64 / L) * row_bytes);
+#pragma unroll
+        for (int q = 0; q < PERIOD; ++q) {
+            const int slot = (NW * q + wave) * 64 + lane;
+            const int r = slot / L;
+            const int c = (slot % L) ^ swz<L>(r);
+            voff0[q] = c < valid_chunks ? (uint32_t)(r * row_bytes + c * 16) : kOob;
+        }
+        row_step = (uint32_t)(PERIOD * RPR * row_bytes);
     }
     __device__ __forceinline__ void issue(rsrc_t rs, unsigned char* tile, int wave) const {
-        issue_part(rs, tile, wave, 0, PER_WAVE);
-    }
-    // copies u0 <= u < u1 only (to spread a tile's copies over a step)
-    __device__ __forceinline__ void issue_part(rsrc_t rs, unsigned char* tile, int wave, int u0, int u1) const {
 #pragma unroll
         for (int u = 0; u < PER_WAVE; ++u)
-            if (u >= u0 && u < u1 && (LOADS % NW == 0 || u * NW + wave < LOADS))
-                dma16(rs, tile + (u * NW + wave) * 1024, voff0 + u * row_step);
+            if (LOADS % NW == 0 || u * NW + wave < LOADS)
+                dma16(rs, tile + (u * NW + wave) * 1024, voff0[u % PERIOD] + (u / PERIOD) * row_step);
     }
 };
 
@@ -642,6 +646,7 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
 #ifndef SDPA_DKDV_SPLIT
 #define SDPA_DKDV_SPLIT 1
 #endif
+
 
 template <int DQK, int DV>
 struct DkvDmaCfg {
@@ -1202,14 +1207,24 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
             if (n == 0 && nsteps > 1) wait_vm_n<LPS>();
             else wait_vm();
             __syncthreads();
-            if (n >= 1 && n + 1 < nsteps) issue(n + 1);
+            // copies of block n + 1 in two bursts: Q (+ a stats / delta row)
+            // now, dO after the first sub-tile
+            const bool cp = n >= 1 && n + 1 < nsteps;
+            const int qn = q_top - (n + 1) * BQ;
+            unsigned char* stn = smem + ((n + 1) % NSTAGE) * Cfg::STAGE;
+            if (cp) {
+                qd.issue(make_rsrc(Qb + (size_t)qn * D_qk, (long long)(S_q - qn) * D_qk * 2), stn, kw);
+                if (kw == 0) dma4(make_rsrc(st2b + qn, (long long)(S_q - qn) * 4), stn + Cfg::QB + Cfg::OB, lane * 4);
+                if (kw == 1)
+                    dma4(make_rsrc(deltab + qn, (long long)(S_q - qn) * 4), stn + Cfg::QB + Cfg::OB + BQ * 4, lane * 4);
+            }
             if (n == 0) continue;
             const int m = n - 1;
             const int q0 = q_top - m * BQ;
             const uint32_t qbase = (uint32_t)((m % NSTAGE) * Cfg::STAGE);
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-                if (sub_live(q0 + 32 * t)) sub(qbase, m, t);
+            if (sub_live(q0)) sub(qbase, m, 0);
+            if (cp) od.issue(make_rsrc(dOb + (size_t)qn * D_v, (long long)(S_q - qn) * D_v * 2), stn + Cfg::QB, kw);
+            if (sub_live(q0 + 32)) sub(qbase, m, 1);
         }
         if (key_ok) {
             half_t* dKb = static_cast<half_t*>(p.dk) + ((size_t)b * S_kv + my_k) * D_qk;
