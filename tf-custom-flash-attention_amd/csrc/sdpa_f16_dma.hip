@@ -49,6 +49,11 @@ namespace {
 // the word-3 configuration of a raw buffer on gfx950.
 typedef int rsrc_t __attribute__((ext_vector_type(4)));
 
+// MFMA operands read ahead from LDS (in MFMAs) by the fenced chains.
+#ifndef SDPA_RD
+#define SDPA_RD 4
+#endif
+
 // A voffset at or past num_records: the load returns zero and touches nothing.
 constexpr uint32_t kOob = 0x80000000u;
 // Lazy-rescale threshold of the forward's running maximum (log2 units).
@@ -571,63 +576,102 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
 #pragma unroll
     for (int dt = 0; dt < DQK / 32; ++dt) dqacc[dt] = floatx16{};
 
-    for (int step = 0; step < nsteps; ++step) {
+    // dS of one 32-key sub-tile; the rows of the accumulators are keys
+    // k0 + 8 (r/4) + 4 hh + r%4.  PART: the causal mask or the key tail cuts it.
+    auto elem = [&]<bool PART>(const floatx16& sacc, const floatx16& dpacc, int k0, half8& ds0, half8& ds1) {
+        uint64_t st_blk = DROP ? st_lane + (uint64_t)k0 * kLcgMul : 0;
+        // hash states after the MFMAs (hoisted above them they hold 32 VGPRs)
+        if constexpr (DROP) asm volatile("" : "+v"(st_blk) : "v"(dpacc[15]));
+        uint32_t w[8];
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            float ds2[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int rr = r + e;
+                float x = __builtin_fmaf(sacc[rr], sl2, nst);
+                if constexpr (PART) {
+                    const int key = k0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
+                    if (key >= S_kv || (CAUSAL && key > my_q)) x = -INFINITY;
+                }
+                const float pr = fast_exp2(x);
+                float tt;
+                if constexpr (DROP) {
+                    const bool keep = lcg_keep(st_blk + (uint64_t)(8 * (rr >> 2) + (rr & 3)) * kLcgMul, thr);
+                    tt = keep ? __builtin_fmaf(dpacc[rr], ksc, -delta) : -delta;
+                } else {
+                    tt = dpacc[rr] - delta;
+                }
+                ds2[e] = pr > kEps ? pr * tt : 0.f;
+            }
+            w[r >> 1] = pack_h2(ds2[0], ds2[1]);
+        }
+        ds0 = half8_of(w[0], w[1], w[2], w[3]);
+        ds1 = half8_of(w[4], w[5], w[6], w[7]);
+    };
+    // Sub-tile t of the step at kbase.  The S and dP chains read their A
+    // operands RD MFMAs ahead, and scheduling fences keep the reads there
+    // (left to itself the compiler reads each operand just before its MFMA
+    // and waits out the whole LDS latency every time); the transposed reads
+    // for dQ go out before the element-wise work and land during it.
+    constexpr int NK = DQK / 16, NV = DV / 16, RD = SDPA_RD;
+    auto sub = [&]<bool PART>(uint32_t kbase, int k0, int t) {
+        const uint32_t aK = kbase + swK.row, aV = kbase + Cfg::KB + swV.row;
+        const uint32_t aK0 = kbase + swK.tr0, aK1 = kbase + swK.tr1;
+        auto rd = [&](int i) { return i < NK ? lds_row<LK>(aK, i, 32 * t) : lds_row<LV>(aV, i - NK, 32 * t); };
+        half8 op[NK + NV];
+#pragma unroll
+        for (int i = 0; i < RD; ++i) op[i] = rd(i);
+        __builtin_amdgcn_sched_barrier(0);
+        floatx16 sacc = floatx16{}, dpacc = floatx16{};
+#pragma unroll
+        for (int i = 0; i < NK + NV; ++i) {
+            if (i + RD < NK + NV) op[i + RD] = rd(i + RD);
+            if (i < NK) sacc = mfma_f16(op[i], qreg[i], sacc);
+            else dpacc = mfma_f16(op[i], doreg[i - NK], dpacc);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        half8 at[2][DQK / 32];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int dt = 0; dt < DQK / 32; ++dt) at[j][dt] = lds_tr<LK>(aK0, aK1, dt, 32 * t + 16 * j);
+        __builtin_amdgcn_sched_barrier(0);
+        half8 ds0, ds1;
+        elem.template operator()<PART>(sacc, dpacc, k0, ds0, ds1);
+#pragma unroll
+        for (int dt = 0; dt < DQK / 32; ++dt) {
+            dqacc[dt] = mfma_f16(at[0][dt], ds0, dqacc[dt]);
+            dqacc[dt] = mfma_f16(at[1][dt], ds1, dqacc[dt]);
+        }
+    };
+    auto sync_step = [&](int step) {
         wait_vm();
         __syncthreads();
         if (step + 1 < nsteps) issue(step + 1);
+    };
+    // Steps whose 64 keys are all visible to all 32 queries of the wave come
+    // first (no mask code); the causal diagonal and the key tail follow.
+    const int full_lim = CAUSAL ? min(qw0 - (BN - 1), S_kv - BN) : S_kv - BN;
+    const int n_full = qw0 >= S_q ? 0 : min(nsteps, full_lim < 0 ? 0 : full_lim / BN + 1);
+    int step = 0;
+    for (; step < n_full; ++step) {
+        sync_step(step);
+        const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE);
+        sub.template operator()<false>(kbase, step * BN, 0);
+        sub.template operator()<false>(kbase, step * BN + 32, 1);
+    }
+    for (; step < nsteps; ++step) {
+        sync_step(step);
         if (qw0 >= S_q) continue;
         const int kv0 = step * BN;
-        const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE), vbase = kbase + Cfg::KB;
-        const uint32_t aK = kbase + swK.row, aV = vbase + swV.row;
-        const uint32_t aK0 = kbase + swK.tr0, aK1 = kbase + swK.tr1;
-
+        const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int k0 = kv0 + 32 * t;
             if (!(k0 < S_kv && (!CAUSAL || k0 <= qw0 + 31))) continue;
-            const bool part = k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0);
-
-            floatx16 sacc = floatx16{}, dpacc = floatx16{};
-#pragma unroll
-            for (int ks = 0; ks < DQK / 16; ++ks)
-                sacc = mfma_f16(lds_row<LK>(aK, ks, 32 * t), qreg[ks], sacc);
-#pragma unroll
-            for (int ks = 0; ks < DV / 16; ++ks)
-                dpacc = mfma_f16(lds_row<LV>(aV, ks, 32 * t), doreg[ks], dpacc);
-
-            // rows of the accumulators are keys k0 + 8 (r/4) + 4 hh + r%4
-            const uint64_t st_blk = DROP ? st_lane + (uint64_t)k0 * kLcgMul : 0;
-            uint32_t w[8];
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                float ds2[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int rr = r + e;
-                    float x = __builtin_fmaf(sacc[rr], sl2, nst);
-                    if (part) {
-                        const int key = k0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
-                        if (key >= S_kv || (CAUSAL && key > my_q)) x = -INFINITY;
-                    }
-                    const float pr = fast_exp2(x);
-                    float tt;
-                    if constexpr (DROP) {
-                        const bool keep = lcg_keep(st_blk + (uint64_t)(8 * (rr >> 2) + (rr & 3)) * kLcgMul, thr);
-                        tt = keep ? __builtin_fmaf(dpacc[rr], ksc, -delta) : -delta;
-                    } else {
-                        tt = dpacc[rr] - delta;
-                    }
-                    ds2[e] = pr > kEps ? pr * tt : 0.f;
-                }
-                w[r >> 1] = pack_h2(ds2[0], ds2[1]);
-            }
-            const half8 dsb0 = half8_of(w[0], w[1], w[2], w[3]);
-            const half8 dsb1 = half8_of(w[4], w[5], w[6], w[7]);
-#pragma unroll
-            for (int dt = 0; dt < DQK / 32; ++dt) {
-                dqacc[dt] = mfma_f16(lds_tr<LK>(aK0, aK1, dt, 32 * t), dsb0, dqacc[dt]);
-                dqacc[dt] = mfma_f16(lds_tr<LK>(aK0, aK1, dt, 32 * t + 16), dsb1, dqacc[dt]);
-            }
+            if (k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0)) sub.template operator()<true>(kbase, k0, t);
+            else sub.template operator()<false>(kbase, k0, t);
         }
     }
 
