@@ -1,499 +1,41 @@
-// sdpa_f16_dma.hip -- fp16 Sdpa / SdpaGrad kernels for gfx950 that stream
-// their K/V (forward, dQ) or Q/dO (dK/dV) tiles from HBM straight into LDS.
+// sdpa_f16_dma.hip -- fp16 SdpaGrad kernels for gfx950 that stream their
+// K/V (dQ) or Q/dO (dK/dV) tiles from HBM straight into LDS (the forward is
+// in sdpa_f16_fwd.hip; the copy machinery in sdpa_dma.h).
 //
-// These are the production kernels for the fp16 op whenever every feature
-// width is a multiple of 8 and every tensor is 16-byte aligned (the shapes
-// the reference's MHA layer produces, sdpa_fwd.cu.cc:191-215 dispatch up to
-// D = 128).  Other fp16 shapes use the register-staged kernels of
-// sdpa_fwd.hip / sdpa_bwd.hip, which accept any D.
+// These are the production backward kernels for the fp16 op whenever every
+// feature width is a multiple of 8 and every tensor is 16-byte aligned (the
+// shapes the reference's MHA layer produces, sdpa_fwd.cu.cc:191-215 dispatch
+// up to D = 128).  Other fp16 shapes use the register-staged kernels of
+// sdpa_bwd.hip, which accept any D.
 //
-// Data movement.  Tiles are copied by buffer_load_dwordx4 ... lds: lane L of
-// a wave writes 16 bytes to LDS at (wave base + 16 L), and each lane picks
-// the global chunk that belongs there, so the LDS image comes out in the
-// chunk-swizzled layout of swz_off() (conflict-free row and transpose reads)
-// without passing through VGPRs.  The buffer descriptor of every tile starts
-// at the tile's first row and ends at the end of the batch row, so rows past
-// S and columns past D read as zero: tails need no branches.  Forward and dQ
-// use two LDS stages (the copy of step n+1 is in flight while step n is
-// multiplied, one barrier per step); dK/dV uses a ring of three.
+// The buffer descriptor of every tile starts at the tile's first row and ends
+// at the end of the batch row, so rows past S and columns past D read as
+// zero: tails need no branches.  dQ uses two LDS stages (the copy of step n+1
+// is in flight while step n is multiplied, one barrier per step); dK/dV uses
+// a ring of three.
 //
 // Work order.  Workgroup ids are remapped so that each XCD (ids are dealt
 // round-robin over the 8 XCDs) walks whole batch rows: all tiles of a batch
-// row run on one XCD and share its L2 copy of the streamed operands.  Under
-// causal masking the heaviest tiles of a batch row go first.
+// row run on one XCD and share its L2 copy of the streamed operands.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16, fp32 accumulation; the lane
 // layouts are listed in sdpa_device.h):
-//   forward, per wave of 32 queries (lane = query):
-//     S^T = K Q^T, online softmax over keys, O^T += V^T P~^T
-//   dQ, per wave of 32 queries:
+//   dQ, per wave of 32 queries (lane = query):
 //     S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T
 //   dK/dV, per group of 32 keys (lane = key):
 //     S = Q K^T, dP = dO V^T, dV^T += dO^T P~, dK^T += Q^T dS
 //     (one wave per group, or at a 128-wide side two: one for S, P and dV,
 //     one for dP, dS and dK)
-// Element semantics are those of the reference (sdpa/sdpa_fwd.cu.cc:93-173,
-// sdpa/sdpa_bwd.cu.cc:130-170, 291-327), restated in sdpa_fwd.hip and
-// sdpa_bwd.hip.
+// Element semantics are those of the reference (sdpa/sdpa_bwd.cu.cc:130-170,
+// 291-327), restated in sdpa_bwd.hip.
 #include <type_traits>
 
-#include "sdpa_device.h"
+#include "sdpa_dma.h"
 #include "sdpa_launch.h"
 #include "sdpa_params.h"
-#include "sdpa_tile.h"
 
 namespace sdpa {
 namespace {
-
-// Buffer descriptor (four SGPRs): base address, stride 0, num_records, and
-// the word-3 configuration of a raw buffer on gfx950.
-typedef int rsrc_t __attribute__((ext_vector_type(4)));
-
-// MFMA operands read ahead from LDS (in MFMAs) by the fenced chains.
-#ifndef SDPA_RD
-#define SDPA_RD 4
-#endif
-
-// A voffset at or past num_records: the load returns zero and touches nothing.
-constexpr uint32_t kOob = 0x80000000u;
-// Lazy-rescale threshold of the forward's running maximum (log2 units).
-constexpr float kTauF = 8.0f;
-
-extern __shared__ __attribute__((aligned(1024))) unsigned char smem[];
-
-// Raw buffer descriptor over [base, base + bytes); every field is wave-uniform.
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, long long bytes) {
-    const int n = bytes <= 0 ? 0 : (bytes >= 0x7FFFFFFFLL ? 0x7FFFFFFF : (int)bytes);
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    return (rsrc_t){__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
-                    __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu)),
-                    __builtin_amdgcn_readfirstlane(n), 0x00020000};
-}
-
-// LDS byte address of a pointer into smem.
-__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
-    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
-    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(base + (uint32_t)(p - smem)));
-}
-
-// 16 (or 4) bytes per lane from byte offset voff into LDS at wave_dst + 16 L
-// (4 L).  The copies are issued from inline assembly: the compiler does not
-// track them, so it adds no vmcnt waits of its own in front of later LDS
-// reads (with the builtin it waits for every copy in flight before each
-// ds_read_b64_tr_b16).  The kernels order copies and reads themselves: a
-// stage is read only after wait_vm / wait_vm_n and a barrier, and a copy
-// into a stage is issued only after a barrier that follows its last read.
-// M0 holds the LDS base of the copy; the s_nop covers the M0 -> LDS-DMA hazard.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(rsrc_t r, unsigned char* wave_dst, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds_addr(wave_dst)), "v"(voff), "s"(r)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(rsrc_t r, unsigned char* wave_dst, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds_addr(wave_dst)), "v"(voff), "s"(r)
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
-// s_waitcnt vmcnt(0): this wave's copies (and loads) have landed.
-__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// Per-lane global offsets of one ROWS x (8 L) fp16 tile copied by NW waves.
-// LDS chunk slot p (16 bytes) of the tile is row p / L, position p % L; it
-// receives global chunk (p % L) ^ swz<L>(row) of that row.  Copy u of wave w
-// fills slots (NW u + w) * 64 + lane, i.e. rows (NW u + w) * 64 / L + lane / L.
-// The swizzle term depends on the row modulo 16, so it repeats every PERIOD
-// copies (PERIOD = 1 when a round of NW copies spans a multiple of 16 rows):
-// PERIOD offsets per lane plus whole rounds of rows cover all of the wave's
-// copies.
-template <int ROWS, int L, int NW>
-struct TileDma {
-    static constexpr int LOADS = ROWS * L / 64;  // wave-sized copies per tile
-    static constexpr int PER_WAVE = (LOADS + NW - 1) / NW;
-    static constexpr int MIN_PER_WAVE = LOADS / NW;  // copies issued by every wave
-    static constexpr int RPR = NW * 64 / L;          // rows per round of NW copies
-    static constexpr int PERIOD = RPR % 16 == 0 ? 1 : 16 / RPR;
-    static_assert(RPR % 16 == 0 || 16 % RPR == 0, "round must divide or be a multiple of 16 rows");
-    uint32_t voff0[PERIOD];  // offsets of copies 0 .. PERIOD-1 (kOob for chunks past D)
-    uint32_t row_step;       // bytes between copies u and u + PERIOD
-
-    // row_bytes: global row pitch; valid_chunks: 16-byte chunks inside D.
-    __device__ __forceinline__ void init(int wave, int lane, int row_bytes, int valid_chunks) {
-#pragma unroll
-        for (int q = 0; q < PERIOD; ++q) {
-            const int slot = (NW * q + wave) * 64 + lane;
-            const int r = slot / L;
-            const int c = (slot % L) ^ swz<L>(r);
-            voff0[q] = c < valid_chunks ? (uint32_t)(r * row_bytes + c * 16) : kOob;
-        }
-        row_step = (uint32_t)(PERIOD * RPR * row_bytes);
-    }
-    __device__ __forceinline__ void issue(rsrc_t rs, unsigned char* tile, int wave) const {
-#pragma unroll
-        for (int u = 0; u < PER_WAVE; ++u)
-            if (LOADS % NW == 0 || u * NW + wave < LOADS)
-                dma16(rs, tile + (u * NW + wave) * 1024, voff0[u % PERIOD] + (u / PERIOD) * row_step);
-    }
-};
-
-// s_waitcnt vmcnt(N): at most N of this wave's loads still in flight.
-template <int N>
-__device__ __forceinline__ void wait_vm_n() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Workgroup id -> (batch, tile), XCD-major: XCD x (ids x, x+8, ...) owns a
-// contiguous range of the batch-major tile list.  `reverse` issues the tiles
-// of a batch row last-first.
-__device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles, bool reverse, int& b, int& t) {
-    const int xcd = bid & 7, local = bid >> 3;
-    const int per = nblocks >> 3, rem = nblocks & 7;
-    const int lin = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-    b = lin / tiles;
-    const int r = lin - b * tiles;
-    t = reverse ? tiles - 1 - r : r;
-}
-
-// Two fp32 values -> one dword of two RNE-rounded halves (v_cvt_pk_f16_f32).
-__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, half2v));
-}
-
-__device__ __forceinline__ half8 half8_of(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) {
-    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-    return __builtin_bit_cast(half8, (u4){w0, w1, w2, w3});
-}
-
-// Per-lane LDS byte offsets of the MFMA A-operand reads from a swizzled
-// fp16 tile with L 16-byte chunks per row (see swz_off).  The swizzle only
-// permutes chunks inside a 16 L-byte row and every tile base is a multiple of
-// 256 bytes, so each read is (tile base + lane term) ^ constant, with the
-// tile's row offset in the instruction's immediate field:
-//   row read,  rows R0 + l32 (R0 % 16 == 0), features 16 ks + 8 hh .. +7:
-//              ((base + row) ^ (32 ks)) + 16 L R0
-//   transposed read of rows R0 + 16 s + {tr_row, tr_row + 8} (see
-//   lds_read_tr), features 32 dt + tr_col:
-//              ((base + tr[j]) ^ (64 dt)) + 16 L (R0 + 16 s)
-template <int L>
-struct SwzLane {
-    uint32_t row, tr0, tr1;
-    __device__ __forceinline__ void init(int lane) {
-        const int l32 = lane & 31, hh = lane >> 5;
-        row = (uint32_t)(l32 * 16 * L + 16 * (hh ^ swz<L>(l32)));
-        const int g16 = lane >> 4, i16 = lane & 15;
-        const int tr_row = 4 * (g16 >> 1) + (i16 >> 2);
-        const int c = 2 * (g16 & 1) + ((i16 & 3) >> 1);  // chunk of column tr_col within 32 features
-        const int sub = 8 * (i16 & 1);                   // byte of column tr_col within its chunk
-        tr0 = (uint32_t)(tr_row * 16 * L + 16 * (c ^ swz<L>(tr_row)) + sub);
-        tr1 = (uint32_t)((tr_row + 8) * 16 * L + 16 * (c ^ swz<L>(tr_row + 8)) + sub);
-    }
-};
-
-// max(x, 0) of eight finite halves as a signed 16-bit max on their bit
-// patterns (a set sign bit is a negative int16), one v_pk_max_i16 per pair.
-__device__ __forceinline__ half8 relu_h8(half8 x) {
-    typedef short short8 __attribute__((ext_vector_type(8)));
-    return __builtin_bit_cast(half8, __builtin_elementwise_max(__builtin_bit_cast(short8, x), short8{}));
-}
-
-// Row-read A operand: rows R0 + l32 (R0 % 16 == 0), k-step ks.
-// `a` = tile base + SwzLane::row.
-template <int L>
-__device__ __forceinline__ half8 lds_row(uint32_t a, int ks, int R0) {
-    return *reinterpret_cast<const half8*>(smem + ((a ^ (uint32_t)(32 * ks)) + 16 * L * R0));
-}
-
-// Transposed A operand: tile rows R0 .. R0 + 15 (R0 % 16 == 0) in the order
-// of the accumulator layout, features 32 dt + (0..31).
-// a0 / a1 = tile base + SwzLane::tr0 / tr1.
-template <int L>
-__device__ __forceinline__ half8 lds_tr(uint32_t a0, uint32_t a1, int dt, int R0) {
-    const half4 x0 = lds_read_tr(reinterpret_cast<const half_t*>(smem + ((a0 ^ (uint32_t)(64 * dt)) + 16 * L * R0)));
-    const half4 x1 = lds_read_tr(reinterpret_cast<const half_t*>(smem + ((a1 ^ (uint32_t)(64 * dt)) + 16 * L * R0)));
-    return __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-// Store 16 fp32 accumulator rows of a C^T tile (lane = output row, in-lane =
-// features 32 dt + 8 g + 4 hh + e) as fp16 with a common factor.
-template <int DN>
-__device__ __forceinline__ void store_rows_f16(half_t* dst, const floatx16 (&acc)[DN / 32], float f, int hh) {
-#pragma unroll
-    for (int dt = 0; dt < DN / 32; ++dt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            half4 hv;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) hv[e] = (half_t)(acc[dt][4 * g + e] * f);
-            *reinterpret_cast<half4*>(dst + 32 * dt + 8 * g + 4 * hh) = hv;
-        }
-}
-
-// Same, columns >= ncols not written (D < padded width).
-template <int DN>
-__device__ __forceinline__ void store_rows_f16_n(half_t* dst, const floatx16 (&acc)[DN / 32], float f, int hh,
-                                                 int ncols) {
-#pragma unroll
-    for (int dt = 0; dt < DN / 32; ++dt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int d0 = 32 * dt + 8 * g + 4 * hh;
-            if (d0 < ncols) {
-                half4 hv;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) hv[e] = (half_t)(acc[dt][4 * g + e] * f);
-                *reinterpret_cast<half4*>(dst + d0) = hv;
-            }
-        }
-}
-
-// ===========================================================================
-// Forward
-// ===========================================================================
-template <int DQK, int DV>
-struct FwdDmaCfg {
-    // NW waves of 32 queries each; K/V blocks of BN keys in an NSTAGE-deep
-    // LDS ring (the copy of block n + NSTAGE - 1 is issued at step n).
-#ifndef SDPA_FWD_NW
-#define SDPA_FWD_NW 4
-#endif
-#ifndef SDPA_FWD_NSTAGE
-#define SDPA_FWD_NSTAGE 2
-#endif
-    static constexpr int NW = SDPA_FWD_NW, NSTAGE = SDPA_FWD_NSTAGE;
-    static constexpr int NT = 64 * NW, BM = 32 * NW, BN = 64;
-    static constexpr int LK = DQK / 8, LV = DV / 8;
-    static constexpr int KB = BN * DQK * 2, VB = BN * DV * 2, STAGE = KB + VB;
-    static constexpr size_t LDS_BYTES = NSTAGE * (size_t)STAGE;
-};
-
-template <int DQK, int DV, bool CAUSAL, bool DROP>
-__global__ __launch_bounds__((FwdDmaCfg<DQK, DV>::NT)) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
-    using Cfg = FwdDmaCfg<DQK, DV>;
-    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV;
-
-    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
-    const int tiles = (S_q + BM - 1) / BM;
-    int b, qt;
-    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, b, qt);
-    const int q0 = qt * BM, qw0 = q0 + 32 * wave, my_q = qw0 + l32;
-
-    const half_t* Qb = static_cast<const half_t*>(p.q) + (size_t)b * S_q * D_qk;
-    const half_t* Kb = static_cast<const half_t*>(p.k) + (size_t)b * S_kv * D_qk;
-    const half_t* Vb = static_cast<const half_t*>(p.v) + (size_t)b * S_kv * D_v;
-
-    // The running maximum is taken on raw scores q.k, which needs a
-    // non-negative factor: for scale < 0 the queries are negated in
-    // registers (exact) and |scale| used.  A zero factor is replaced by
-    // 1e-30, which leaves every probability 1 to within 1e-26.
-    const float sl2_raw = p.c.scale_log2;
-    const bool neg = sl2_raw < 0.f;
-    const float sl2 = (sl2_raw == 0.f) ? 1e-30f : fabsf(sl2_raw);
-
-    half8 qreg[DQK / 16];
-#pragma unroll
-    for (int ks = 0; ks < DQK / 16; ++ks) {
-        half8 v = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Qb, my_q, S_q, 16 * ks + 8 * hh, D_qk, D_qk));
-        qreg[ks] = neg ? -v : v;
-    }
-
-    constexpr int NW = Cfg::NW, NSTAGE = Cfg::NSTAGE;
-    TileDma<BN, LK, NW> kd;
-    TileDma<BN, LV, NW> vd;
-    // copies issued by every wave per step (waits count only those)
-    constexpr int LPS = TileDma<BN, LK, NW>::MIN_PER_WAVE + TileDma<BN, LV, NW>::MIN_PER_WAVE;
-    kd.init(wave, lane, D_qk * 2, D_qk / 8);
-    vd.init(wave, lane, D_v * 2, D_v / 8);
-    const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
-    const int nsteps = (kv_end + BN - 1) / BN;
-    auto issue = [&](int step) {
-        const int kv0 = step * BN;
-        unsigned char* st = smem + (step % NSTAGE) * Cfg::STAGE;
-        kd.issue(make_rsrc(Kb + (size_t)kv0 * D_qk, (long long)(S_kv - kv0) * D_qk * 2), st, wave);
-        vd.issue(make_rsrc(Vb + (size_t)kv0 * D_v, (long long)(S_kv - kv0) * D_v * 2), st + Cfg::KB, wave);
-    };
-#pragma unroll
-    for (int i = 0; i < NSTAGE - 1; ++i)
-        if (i < nsteps) issue(i);
-
-    floatx16 oacc[DV / 32];
-#pragma unroll
-    for (int dt = 0; dt < DV / 32; ++dt) oacc[dt] = floatx16{};
-    float m_run = kMaxSentinel, l_run = 0.f;
-
-    // Dropout hash of (my_q, key 4 hh); element (key kv0 + c) adds (kv0 + c) A.
-    const uint64_t st_lane = DROP ? lcg_state(p.c.seed_offset, (uint64_t)b * S_q + my_q, (uint64_t)S_kv, 4 * hh) : 0;
-    const uint32_t thr = p.c.drop_threshold;
-
-    SwzLane<LK> swK;
-    SwzLane<LV> swV;
-    swK.init(lane);
-    swV.init(lane);
-
-    // Softmax of one 32-key sub-tile t (scores s, raw q.k; masked keys set to
-    // -inf by the caller): per-lane lazy maximum m_use (moves only when the
-    // block maximum exceeds the running one by more than 2^kTauF), alpha =
-    // exp2(m_run - m_use), P = exp2(s sl2 - m_use), the undropped sum and the
-    // dropped, fp16-packed B operands of the PV product.
-    auto softmax_sub = [&](const floatx16& sc, int t, uint64_t st_blk, float& m_use, float& alpha, float& lsum,
-                           half8& pb0, half8& pb1) {
-        float mx = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
-#pragma unroll
-        for (int r = 3; r < 15; r += 2) mx = fmaxf(mx, fmaxf(sc[r], sc[r + 1]));
-        mx = fmaxf(mx, sc[15]);
-        mx = xhalf_max(mx) * sl2;
-        m_use = (mx > m_run + kTauF) ? fmaxf(m_run, mx) : m_run;
-        alpha = fast_exp2(m_run - m_use);
-        const float nm = -m_use;
-        uint32_t w[8];
-        float lq[4];
-#pragma unroll
-        for (int r = 0; r < 16; r += 4) {
-            float pq[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) pq[e] = fast_exp2(__builtin_fmaf(sc[r + e], sl2, nm));
-            lq[r >> 2] = (pq[0] + pq[1]) + (pq[2] + pq[3]);
-            if constexpr (DROP) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int c = 32 * t + 8 * (r >> 2) + e;
-                    pq[e] = lcg_keep(st_blk + (uint64_t)c * kLcgMul, thr) ? pq[e] : 0.f;
-                }
-            }
-            w[r >> 1] = pack_h2(pq[0], pq[1]);
-            w[(r >> 1) + 1] = pack_h2(pq[2], pq[3]);
-        }
-        lsum = (lq[0] + lq[1]) + (lq[2] + lq[3]);
-        pb0 = half8_of(w[0], w[1], w[2], w[3]);
-        pb1 = half8_of(w[4], w[5], w[6], w[7]);
-    };
-    // Mask of sub-tile t: keys past S_kv and, causal, keys after the query.
-    auto mask_sub = [&](floatx16& sc, int kv0, int t) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * hh + (r & 3);
-            if (key >= S_kv || (CAUSAL && key > my_q)) sc[r] = -INFINITY;
-        }
-    };
-    // After a sub-tile's PV operands are formed: rescale the output (rare,
-    // wave-uniform branch) and fold the sub-tile into the running sum.
-    auto commit_sub = [&](float m_use, float alpha, float lsum) {
-        if (wave_any(alpha != 1.f)) {
-#pragma unroll
-            for (int dt = 0; dt < DV / 32; ++dt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-        }
-        l_run = __builtin_fmaf(l_run, alpha, lsum);
-        m_run = m_use;
-    };
-
-    // One step = 64 keys as two 32-key sub-tiles, written in software-pipeline
-    // order so that each MFMA group has independent work next to it (a wave
-    // issues in order; the compiler interleaves within these spans):
-    //   R1  S(0) = K0 Q^T           with LDS reads of K1
-    //   R2  S(1) = K1 Q^T           with softmax(0), LDS reads of V0^T
-    //   R3  O^T += V0^T P0~^T       with softmax(1), LDS reads of V1^T
-    //   R4  O^T += V1^T P1~^T
-    // The rescale of O by sub-tile 1's new maximum commutes with the pending
-    // PV(0) accumulation, so it is applied after R3.
-    auto fwd_step = [&]<bool PART>(int kv0, uint32_t aK, uint32_t aV0, uint32_t aV1) {
-        const bool part0 = PART && (kv0 + 32 > S_kv || (CAUSAL && kv0 + 31 > qw0));
-        const bool part1 = PART && (kv0 + 64 > S_kv || (CAUSAL && kv0 + 63 > qw0));
-        const uint64_t st_blk = DROP ? st_lane + (uint64_t)kv0 * kLcgMul : 0;
-        half8 ak0[DQK / 16], ak1[DQK / 16];
-#pragma unroll
-        for (int ks = 0; ks < DQK / 16; ++ks) ak0[ks] = lds_row<LK>(aK, ks, 0);
-        // R1
-        floatx16 s0 = floatx16{}, s1 = floatx16{};
-#pragma unroll
-        for (int ks = 0; ks < DQK / 16; ++ks) {
-            s0 = mfma_f16(ak0[ks], qreg[ks], s0);
-            ak1[ks] = lds_row<LK>(aK, ks, 32);
-        }
-        // R2
-#pragma unroll
-        for (int ks = 0; ks < DQK / 16; ++ks) s1 = mfma_f16(ak1[ks], qreg[ks], s1);
-        half8 av0[2][DV / 32], av1[2][DV / 32];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int dt = 0; dt < DV / 32; ++dt) av0[j][dt] = lds_tr<LV>(aV0, aV1, dt, 16 * j);
-        if (part0) mask_sub(s0, kv0, 0);
-        float mu0, al0, ls0;
-        half8 p00, p01;
-        softmax_sub(s0, 0, st_blk, mu0, al0, ls0, p00, p01);
-        commit_sub(mu0, al0, ls0);
-        // R3
-#pragma unroll
-        for (int dt = 0; dt < DV / 32; ++dt) {
-            oacc[dt] = mfma_f16(av0[0][dt], p00, oacc[dt]);
-            oacc[dt] = mfma_f16(av0[1][dt], p01, oacc[dt]);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int dt = 0; dt < DV / 32; ++dt) av1[j][dt] = lds_tr<LV>(aV0, aV1, dt, 32 + 16 * j);
-        if (part1) mask_sub(s1, kv0, 1);
-        float mu1, al1, ls1;
-        half8 p10, p11;
-        softmax_sub(s1, 1, st_blk, mu1, al1, ls1, p10, p11);
-        commit_sub(mu1, al1, ls1);
-        // R4
-#pragma unroll
-        for (int dt = 0; dt < DV / 32; ++dt) {
-            oacc[dt] = mfma_f16(av1[0][dt], p10, oacc[dt]);
-            oacc[dt] = mfma_f16(av1[1][dt], p11, oacc[dt]);
-        }
-    };
-
-    // Wait for block `step` (at most the copies of the NSTAGE - 2 later blocks
-    // may still be in flight; all of them at the tail), synchronise, and start
-    // the copy of block step + NSTAGE - 1.
-    auto sync_step = [&](int step) {
-        if (step + NSTAGE - 2 < nsteps) wait_vm_n<(NSTAGE - 2) * LPS>();
-        else wait_vm();
-        __syncthreads();
-        if (step + NSTAGE - 1 < nsteps) issue(step + NSTAGE - 1);
-    };
-    // Steps whose 64 keys are all visible to all 32 queries of this wave run
-    // the unmasked variant; the causal diagonal and the key tail come last.
-    const int full_lim = CAUSAL ? min(qw0 - (BN - 1), S_kv - BN) : S_kv - BN;
-    const int n_full = qw0 >= S_q ? 0 : min(nsteps, full_lim < 0 ? 0 : full_lim / BN + 1);
-    const bool live = qw0 < S_q;
-    int step = 0;
-    for (; step < n_full; ++step) {
-        sync_step(step);
-        const uint32_t kbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE), vbase = kbase + Cfg::KB;
-        fwd_step.template operator()<false>(step * BN, kbase + swK.row, vbase + swV.tr0, vbase + swV.tr1);
-    }
-    for (; step < nsteps; ++step) {
-        sync_step(step);
-        const int kv0 = step * BN;
-        if (!live || (CAUSAL && kv0 > qw0 + 31)) continue;  // no visible key in this step
-        const uint32_t kbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE), vbase = kbase + Cfg::KB;
-        fwd_step.template operator()<true>(kv0, kbase + swK.row, vbase + swV.tr0, vbase + swV.tr1);
-    }
-
-    // ---- epilogue: stats = m + log(l + 1e-6), O = acc / l (0 if l <= 1e-6) ----
-    const float l_tot = xhalf_sum(l_run);
-    if (my_q < S_q) {
-        const float m_nat = (l_tot > 0.f) ? m_run * kLn2 : kNegInf;
-        if (hh == 0) p.stats[(size_t)b * S_q + my_q] = m_nat + logf(l_tot + kEps);
-        const float inv = (l_tot > kEps) ? p.c.keep_scale / l_tot : 0.f;
-        half_t* Ob = static_cast<half_t*>(p.o) + ((size_t)b * S_q + my_q) * D_v;
-        if (D_v == DV) store_rows_f16<DV>(Ob, oacc, inv, hh);
-        else store_rows_f16_n<DV>(Ob, oacc, inv, hh, D_v);
-    }
-}
 
 // ===========================================================================
 // Backward, dQ kernel (also writes stats2 and delta to the workspace)
@@ -1283,24 +825,6 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-hipError_t launch_fwd_f16_dma(const FwdParams& p, hipStream_t stream) {
-    const int B = p.s.B, S_q = p.s.S_q;
-    if (B == 0 || S_q == 0) return hipSuccess;
-    return with_dim(p.s.D_qk, [&](auto dqk) {
-        return with_dim(p.s.D_v, [&](auto dv) {
-            return with_bool(p.c.causal != 0, [&](auto c) {
-                return with_bool(p.c.use_dropout != 0, [&](auto d) {
-                    constexpr int DQK = decltype(dqk)::value, DV = decltype(dv)::value;
-                    using Cfg = FwdDmaCfg<DQK, DV>;
-                    const long long n = (long long)((S_q + Cfg::BM - 1) / Cfg::BM) * B;
-                    return launch_kernel<sdpa_fwd_f16_dma_kernel<DQK, DV, decltype(c)::value, decltype(d)::value>>(
-                        (unsigned)n, Cfg::NT, Cfg::LDS_BYTES, stream, p);
-                });
-            });
-        });
-    });
-}
-
 hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream) {
     const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv;
     if (B == 0) return hipSuccess;
