@@ -21,6 +21,7 @@ import math
 import os
 import platform
 import re
+import statistics
 import sys
 import time
 
@@ -123,6 +124,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=512,
                     help="query rows per batch in the CPU baseline sample (0: skip it)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0: auto)")
+    ap.add_argument("--cold-steps", type=int, default=5,
+                    help="extra steps timed with the caches flushed before every kernel (0: skip)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
@@ -212,6 +215,29 @@ def main():
     ms_per_step = total_ms / K
     per = {name: sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(K)) / K
            for j, (name, _) in enumerate(phases)}
+    med = {name: statistics.median(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(K))
+           for j, (name, _) in enumerate(phases)}
+
+    # Cache-cold timing (reported beside the warm, back-to-back figures): before
+    # every kernel a 512 MiB buffer is overwritten, which evicts the operands
+    # from the L2s and from the 256 MB Infinity Cache; only the kernel itself
+    # sits between its events.
+    cold = None
+    if args.cold_steps > 0:
+        flush = torch.empty((512 << 20,), dtype=torch.uint8, device=dev)
+        cev = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * len(phases))]
+               for _ in range(args.cold_steps)]
+        for i in range(args.cold_steps):
+            for j, (_, fn) in enumerate(phases):
+                flush.fill_(i + j)
+                cev[i][2 * j].record(stream)
+                fn()
+                cev[i][2 * j + 1].record(stream)
+        torch.cuda.synchronize()
+        cold = {name: round(statistics.median(cev[i][2 * j].elapsed_time(cev[i][2 * j + 1])
+                                              for i in range(args.cold_steps)), 4)
+                for j, (name, _) in enumerate(phases)}
+        del flush
 
     f_fwd, f_dq, f_dkdv = flops(cfg)
     f_bwd = f_dq + f_dkdv
@@ -264,6 +290,8 @@ def main():
         "fwd_pct_peak": round(100.0 * f_fwd / (fwd_ms * 1e-3) / 1e12 / peak, 2),
         "bwd_pct_peak": round(100.0 * f_bwd / (bwd_ms * 1e-3) / 1e12 / peak, 2),
         "kernel_ms": {k_: round(v_, 4) for k_, v_ in per.items()},
+        "kernel_ms_median": {k_: round(v_, 4) for k_, v_ in med.items()},
+        "kernel_ms_cache_cold": cold,
         "wall_s": round(wall, 3),
         "roofline": {
             "kernel": kernel_symbol,
