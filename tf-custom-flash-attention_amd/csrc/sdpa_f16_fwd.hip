@@ -213,7 +213,8 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
     //   R4  O^T += V1^T P1~^T
     // The rescale of O by sub-tile 1's new maximum commutes with the pending
     // PV(0) accumulation, so it is applied after R3.
-    auto fwd_step = [&]<bool PART>(int kv0, uint32_t so) {
+    // mid(k) marks the end of region k (the copy points of the step).
+    auto fwd_step = [&]<bool PART>(int kv0, uint32_t so, auto&& mid) {
         const bool part0 = PART && (kv0 + 32 > S_kv || (CAUSAL && kv0 + 31 > qw0));
         const bool part1 = PART && (kv0 + 64 > S_kv || (CAUSAL && kv0 + 63 > qw0));
         // Read addresses of this step, formed here (opaque lane terms keep the
@@ -235,6 +236,7 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
             s0 = mfma_f16(ak0[ks], qreg[ks], s0);
             ak1[ks] = ld_b128(rk[ks] + 16 * LK * 32);
         }
+        mid(1);
         // R2
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) s1 = mfma_f16(ak1[ks], qreg[ks], s1);
@@ -249,6 +251,7 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         half8 p00, p01;
         softmax_sub(s0, 0, st_blk, mu0, al0, ls0, p00, p01);
         commit_sub(mu0, al0, ls0);
+        mid(2);
         // R3
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
@@ -265,6 +268,7 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         half8 p10, p11;
         softmax_sub(s1, 1, st_blk, mu1, al1, ls1, p10, p11);
         commit_sub(mu1, al1, ls1);
+        mid(3);
         // R4
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
@@ -274,19 +278,30 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
     };
 
     // Step `step`: wait for its block (the copies of the NSTAGE - 2 later
-    // blocks may still fly; all of them at the tail), synchronise, start the
-    // copy of block step + NSTAGE - 1 into the slot of block step - 1 (every
-    // wave has finished reading it), multiply.
+    // blocks may still fly; all of them at the tail), synchronise, multiply,
+    // and copy block step + NSTAGE - 1 into the slot of block step - 1 (every
+    // wave has finished reading it).  The waves of a workgroup issue their
+    // copies at different points of the step (wave w after region w: at once,
+    // after R1, after R2, after R3): issued together, right after the
+    // barrier, they queue behind each other in the CU's address unit and
+    // stall all four waves at the same time.
     const bool live = qw0 < S_q;
     auto do_step = [&]<bool PART>(int step) {
         const uint32_t so = (uint32_t)((step % NSTAGE) * Cfg::STAGE);
         if (step + NSTAGE - 2 < nsteps) wait_vm_upto((NSTAGE - 2) * cpb);
         else wait_vm();
         __syncthreads();
-        if (step + NSTAGE - 1 < nsteps) issue(step + NSTAGE - 1);
+        const bool cp = step + NSTAGE - 1 < nsteps;
+        static_assert(NW == 4, "one copy point per wave");
+        if (cp && wave == 0) issue(step + NSTAGE - 1);
         const int kv0 = step * BN;
+        auto mid = [&](int k) {
+            if (cp && wave == k) issue(step + NSTAGE - 1);
+        };
         if (!PART || (live && !(CAUSAL && kv0 > qw0 + 31)))  // else: no visible key in this step
-            fwd_step.template operator()<PART>(kv0, so);
+            fwd_step.template operator()<PART>(kv0, so, mid);
+        else if (cp && wave != 0)
+            issue(step + NSTAGE - 1);
         if constexpr (DROP) st_blk += (uint64_t)BN * kLcgMul;
     };
     // Steps whose 64 keys are all visible to all 32 queries of this wave run
