@@ -247,7 +247,7 @@ def main():
     kflops = {"sdpa_fwd": f_fwd, "sdpa_bwd_dq": f_dq, "sdpa_bwd_dkdv": f_dkdv}
     dom = max(per, key=per.get)
     achieved = kflops[dom] / (per[dom] * 1e-3) / 1e12
-    # fp16 shapes with D % 8 == 0 run the DMA-fed kernels (sdpa_f16_dma.hip)
+    # fp16 shapes with D % 8 == 0 run the DMA-fed kernels (sdpa_f16_fwd/dq/dkdv.hip)
     sfx = "f16_dma" if (dt == "f16" and D_qk % 8 == 0 and D_v % 8 == 0) else dt
     # (dK/dV of a feature width above 64 runs the split-role variant)
     kv_sfx = "f16_split" if (sfx == "f16_dma" and max(D_qk, D_v) > 64) else sfx

@@ -1,5 +1,5 @@
 // sdpa_dma.h -- building blocks of the fp16 kernels that stream their tiles
-// from HBM straight into LDS (sdpa_f16_fwd.hip, sdpa_f16_dma.hip): buffer
+// from HBM straight into LDS (sdpa_f16_fwd/dq/dkdv.hip): buffer
 // descriptors and the HBM -> LDS copy instructions, the chunk-swizzled tile
 // layout and its MFMA operand reads, the XCD-aware work order and the fp16
 // stores of accumulator rows.

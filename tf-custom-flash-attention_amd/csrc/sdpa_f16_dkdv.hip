@@ -1,8 +1,9 @@
-// sdpa_f16_dma.hip -- fp16 SdpaGrad kernels for gfx950 that stream their
-// K/V (dQ) or Q/dO (dK/dV) tiles from HBM straight into LDS (the forward is
-// in sdpa_f16_fwd.hip; the copy machinery in sdpa_dma.h).
+// sdpa_f16_dkdv.hip -- fp16 SdpaGrad dK/dV kernels for gfx950 that stream
+// their Q/dO tiles from HBM straight into LDS (the dQ kernel is in
+// sdpa_f16_dq.hip, the forward in sdpa_f16_fwd.hip, the copy machinery in
+// sdpa_dma.h), and the launcher of the fp16 DMA backward.
 //
-// These are the production backward kernels for the fp16 op whenever every
+// These are the production dK/dV kernels for the fp16 op whenever every
 // feature width is a multiple of 8 and every tensor is 16-byte aligned (the
 // shapes the reference's MHA layer produces, sdpa_fwd.cu.cc:191-215 dispatch
 // up to D = 128).  Other fp16 shapes use the register-staged kernels of
@@ -10,22 +11,18 @@
 //
 // The buffer descriptor of every tile starts at the tile's first row and ends
 // at the end of the batch row, so rows past S and columns past D read as
-// zero: tails need no branches.  dQ uses two LDS stages (the copy of step n+1
-// is in flight while step n is multiplied, one barrier per step); dK/dV uses
-// a ring of three.
+// zero: tails need no branches.  Q/dO blocks pass through a ring of three LDS
+// stages.
 //
 // Work order.  Workgroup ids are remapped so that each XCD (ids are dealt
 // round-robin over the 8 XCDs) walks whole batch rows: all tiles of a batch
 // row run on one XCD and share its L2 copy of the streamed operands.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16, fp32 accumulation; the lane
-// layouts are listed in sdpa_device.h):
-//   dQ, per wave of 32 queries (lane = query):
-//     S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T
-//   dK/dV, per group of 32 keys (lane = key):
-//     S = Q K^T, dP = dO V^T, dV^T += dO^T P~, dK^T += Q^T dS
-//     (one wave per group, or at a 128-wide side two: one for S, P and dV,
-//     one for dP, dS and dK)
+// layouts are listed in sdpa_device.h), per group of 32 keys (lane = key):
+//   S = Q K^T, dP = dO V^T, dV^T += dO^T P~, dK^T += Q^T dS
+//   (one wave per group, or at a 128-wide side two: one for S, P and dV,
+//   one for dP, dS and dK)
 // Element semantics are those of the reference (sdpa/sdpa_bwd.cu.cc:130-170,
 // 291-327), restated in sdpa_bwd.hip.
 #include <type_traits>
@@ -36,193 +33,6 @@
 
 namespace sdpa {
 namespace {
-
-// ===========================================================================
-// Backward, dQ kernel (also writes stats2 and delta to the workspace)
-// ===========================================================================
-template <int DQK, int DV>
-struct DqDmaCfg {
-    static constexpr int NT = 256, BM = 128, BN = 64;
-    static constexpr int LK = DQK / 8, LV = DV / 8;
-    static constexpr int KB = BN * DQK * 2, VB = BN * DV * 2, STAGE = KB + VB;
-    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
-};
-
-template <int DQK, int DV, bool CAUSAL, bool DROP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
-    using Cfg = DqDmaCfg<DQK, DV>;
-    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV;
-
-    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
-    const int tiles = (S_q + BM - 1) / BM;
-    int b, qt;
-    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, b, qt);
-    const int q0 = qt * BM, qw0 = q0 + 32 * wave, my_q = qw0 + l32;
-    const size_t row_q = (size_t)b * S_q + my_q;
-
-    const half_t* Qb = static_cast<const half_t*>(p.q) + (size_t)b * S_q * D_qk;
-    const half_t* Ob = static_cast<const half_t*>(p.o) + (size_t)b * S_q * D_v;
-    const half_t* dOb = static_cast<const half_t*>(p.d_o) + (size_t)b * S_q * D_v;
-    const half_t* Kb = static_cast<const half_t*>(p.k) + (size_t)b * S_kv * D_qk;
-    const half_t* Vb = static_cast<const half_t*>(p.v) + (size_t)b * S_kv * D_v;
-
-    half8 qreg[DQK / 16], doreg[DV / 16];
-#pragma unroll
-    for (int ks = 0; ks < DQK / 16; ++ks)
-        qreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Qb, my_q, S_q, 16 * ks + 8 * hh, D_qk, D_qk));
-    float dpart = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < DV / 16; ++ks) {
-        doreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(dOb, my_q, S_q, 16 * ks + 8 * hh, D_v, D_v));
-        const half8 o8 = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Ob, my_q, S_q, 16 * ks + 8 * hh, D_v, D_v));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dpart += (float)doreg[ks][e] * (float)o8[e];
-    }
-    const float delta = xhalf_sum(dpart);
-    const bool row_ok = my_q < S_q;
-    const float stats2 = row_ok ? p.stats[row_q] * kLog2e : INFINITY;
-    if (row_ok && hh == 0) {
-        p.delta[row_q] = delta;
-        p.stats2[row_q] = stats2;
-    }
-    const float sl2 = p.c.scale_log2;
-    const float ksc = p.c.keep_scale;
-    const float nst = -stats2;
-
-    TileDma<BN, LK, 4> kd;
-    TileDma<BN, LV, 4> vd;
-    kd.init(wave, lane, D_qk * 2, D_qk / 8);
-    vd.init(wave, lane, D_v * 2, D_v / 8);
-    const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
-    const int nsteps = (kv_end + BN - 1) / BN;
-    auto issue = [&](int step) {
-        const int kv0 = step * BN;
-        unsigned char* st = smem + (step & 1) * Cfg::STAGE;
-        kd.issue(make_rsrc(Kb + (size_t)kv0 * D_qk, (long long)(S_kv - kv0) * D_qk * 2), st, wave);
-        vd.issue(make_rsrc(Vb + (size_t)kv0 * D_v, (long long)(S_kv - kv0) * D_v * 2), st + Cfg::KB, wave);
-    };
-    if (nsteps > 0) issue(0);
-
-    const uint64_t st_lane = DROP ? lcg_state(p.c.seed_offset, row_q, (uint64_t)S_kv, 4 * hh) : 0;
-    const uint32_t thr = p.c.drop_threshold;
-
-    SwzLane<LK> swK;
-    SwzLane<LV> swV;
-    swK.init(lane);
-    swV.init(lane);
-
-    floatx16 dqacc[DQK / 32];
-#pragma unroll
-    for (int dt = 0; dt < DQK / 32; ++dt) dqacc[dt] = floatx16{};
-
-    // dS of one 32-key sub-tile; the rows of the accumulators are keys
-    // k0 + 8 (r/4) + 4 hh + r%4.  PART: the causal mask or the key tail cuts it.
-    auto elem = [&]<bool PART>(const floatx16& sacc, const floatx16& dpacc, int k0, half8& ds0, half8& ds1) {
-        uint64_t st_blk = DROP ? st_lane + (uint64_t)k0 * kLcgMul : 0;
-        // hash states after the MFMAs (hoisted above them they hold 32 VGPRs)
-        if constexpr (DROP) asm volatile("" : "+v"(st_blk) : "v"(dpacc[15]));
-        uint32_t w[8];
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-            float ds2[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int rr = r + e;
-                float x = __builtin_fmaf(sacc[rr], sl2, nst);
-                if constexpr (PART) {
-                    const int key = k0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
-                    if (key >= S_kv || (CAUSAL && key > my_q)) x = -INFINITY;
-                }
-                const float pr = fast_exp2(x);
-                float tt;
-                if constexpr (DROP) {
-                    const bool keep = lcg_keep(st_blk + (uint64_t)(8 * (rr >> 2) + (rr & 3)) * kLcgMul, thr);
-                    tt = keep ? __builtin_fmaf(dpacc[rr], ksc, -delta) : -delta;
-                } else {
-                    tt = dpacc[rr] - delta;
-                }
-                ds2[e] = pr > kEps ? pr * tt : 0.f;
-            }
-            w[r >> 1] = pack_h2(ds2[0], ds2[1]);
-        }
-        ds0 = half8_of(w[0], w[1], w[2], w[3]);
-        ds1 = half8_of(w[4], w[5], w[6], w[7]);
-    };
-    // Sub-tile t of the step at kbase.  The S and dP chains read their A
-    // operands RD MFMAs ahead, and scheduling fences keep the reads there
-    // (left to itself the compiler reads each operand just before its MFMA
-    // and waits out the whole LDS latency every time); the transposed reads
-    // for dQ go out before the element-wise work and land during it.
-    constexpr int NK = DQK / 16, NV = DV / 16, RD = SDPA_RD;
-    auto sub = [&]<bool PART>(uint32_t kbase, int k0, int t) {
-        const uint32_t aK = kbase + swK.row, aV = kbase + Cfg::KB + swV.row;
-        const uint32_t aK0 = kbase + swK.tr0, aK1 = kbase + swK.tr1;
-        auto rd = [&](int i) { return i < NK ? lds_row<LK>(aK, i, 32 * t) : lds_row<LV>(aV, i - NK, 32 * t); };
-        half8 op[NK + NV];
-#pragma unroll
-        for (int i = 0; i < RD; ++i) op[i] = rd(i);
-        __builtin_amdgcn_sched_barrier(0);
-        floatx16 sacc = floatx16{}, dpacc = floatx16{};
-#pragma unroll
-        for (int i = 0; i < NK + NV; ++i) {
-            if (i + RD < NK + NV) op[i + RD] = rd(i + RD);
-            if (i < NK) sacc = mfma_f16(op[i], qreg[i], sacc);
-            else dpacc = mfma_f16(op[i], doreg[i - NK], dpacc);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        half8 at[2][DQK / 32];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int dt = 0; dt < DQK / 32; ++dt) at[j][dt] = lds_tr<LK>(aK0, aK1, dt, 32 * t + 16 * j);
-        __builtin_amdgcn_sched_barrier(0);
-        half8 ds0, ds1;
-        elem.template operator()<PART>(sacc, dpacc, k0, ds0, ds1);
-#pragma unroll
-        for (int dt = 0; dt < DQK / 32; ++dt) {
-            dqacc[dt] = mfma_f16(at[0][dt], ds0, dqacc[dt]);
-            dqacc[dt] = mfma_f16(at[1][dt], ds1, dqacc[dt]);
-        }
-    };
-    auto sync_step = [&](int step) {
-        wait_vm();
-        __syncthreads();
-        if (step + 1 < nsteps) issue(step + 1);
-    };
-    // Steps whose 64 keys are all visible to all 32 queries of the wave come
-    // first (no mask code); the causal diagonal and the key tail follow.
-    const int full_lim = CAUSAL ? min(qw0 - (BN - 1), S_kv - BN) : S_kv - BN;
-    const int n_full = qw0 >= S_q ? 0 : min(nsteps, full_lim < 0 ? 0 : full_lim / BN + 1);
-    int step = 0;
-    for (; step < n_full; ++step) {
-        sync_step(step);
-        const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE);
-        sub.template operator()<false>(kbase, step * BN, 0);
-        sub.template operator()<false>(kbase, step * BN + 32, 1);
-    }
-    for (; step < nsteps; ++step) {
-        sync_step(step);
-        if (qw0 >= S_q) continue;
-        const int kv0 = step * BN;
-        const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int k0 = kv0 + 32 * t;
-            if (!(k0 < S_kv && (!CAUSAL || k0 <= qw0 + 31))) continue;
-            if (k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0)) sub.template operator()<true>(kbase, k0, t);
-            else sub.template operator()<false>(kbase, k0, t);
-        }
-    }
-
-    if (row_ok) {
-        half_t* dQb = static_cast<half_t*>(p.dq) + row_q * D_qk;
-        if (D_qk == DQK) store_rows_f16<DQK>(dQb, dqacc, p.c.scale, hh);
-        else store_rows_f16_n<DQK>(dQb, dqacc, p.c.scale, hh, D_qk);
-    }
-}
 
 // ===========================================================================
 // Backward, dK/dV kernel (reads stats2 and delta from the workspace)
@@ -834,14 +644,9 @@ hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream
                 return with_bool(p.c.use_dropout != 0, [&](auto d) {
                     constexpr int DQK = decltype(dqk)::value, DV = decltype(dv)::value;
                     constexpr bool CA = decltype(c)::value, DR = decltype(d)::value;
-                    using CQ = DqDmaCfg<DQK, DV>;
                     using CK = DkvDmaCfg<DQK, DV>;
                     hipError_t err = hipSuccess;
-                    if ((phases & kBwdDq) && S_q > 0) {
-                        const long long n = (long long)((S_q + CQ::BM - 1) / CQ::BM) * B;
-                        err = launch_kernel<sdpa_bwd_dq_f16_dma_kernel<DQK, DV, CA, DR>>((unsigned)n, CQ::NT,
-                                                                                   CQ::LDS_BYTES, stream, p);
-                    }
+                    if ((phases & kBwdDq) && S_q > 0) err = launch_bwd_dq_f16_dma(p, stream);
                     if (err == hipSuccess && (phases & kBwdDkDv) && S_kv > 0) {
                         if constexpr (CK::WAVES == 1 && SDPA_DKDV_SPLIT) {
                             using CS = DkvSplitCfg<DQK, DV>;

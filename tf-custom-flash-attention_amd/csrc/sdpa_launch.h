@@ -55,9 +55,12 @@ hipError_t launch_fwd(const FwdParams& p, DType dtype, bool vec, hipStream_t str
 constexpr int kBwdDq = 1, kBwdDkDv = 2;
 hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, int phases, hipStream_t stream);
 
-// fp16 kernels fed by HBM -> LDS copies (sdpa_f16_dma.hip).  They require
-// D_qk and D_v to be multiples of 8 and every tensor 16-byte aligned.
+// fp16 kernels fed by HBM -> LDS copies (sdpa_f16_fwd.hip, sdpa_f16_dq.hip,
+// sdpa_f16_dkdv.hip).  They require D_qk and D_v to be multiples of 8 and
+// every tensor 16-byte aligned.
 hipError_t launch_fwd_f16_dma(const FwdParams& p, hipStream_t stream);
 hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream);
+// dQ phase of launch_bwd_f16_dma (sdpa_f16_dq.hip)
+hipError_t launch_bwd_dq_f16_dma(const BwdParams& p, hipStream_t stream);
 
 }  // namespace sdpa
