@@ -117,6 +117,37 @@ def test_edge_shapes(pkg, O, case):
     run_and_check(pkg, O, c, fp32_sum_allowance=True)
 
 
+def _random_cases(n=24, seed=2024):
+    """Seeded shapes beyond the hand-picked ones: any D in 1..128 (both kernel
+    families), ragged sequence lengths, cross attention, dropout rates, large
+    seed/offset values."""
+    rng = np.random.default_rng(seed)
+    widths = [8, 16, 24, 32, 40, 56, 64, 72, 96, 120, 128]
+    cases = []
+    for i in range(n):
+        dt = "f32" if i % 3 == 0 else "f16"
+        causal = bool(rng.integers(0, 2))
+        S_q = int(rng.integers(1, 320))
+        S_kv = S_q if causal else int(rng.integers(1, 320))
+        D_qk = int(rng.choice(widths)) if rng.random() < 0.7 else int(rng.integers(1, 129))
+        D_v = int(rng.choice(widths)) if rng.random() < 0.7 else int(rng.integers(1, 129))
+        p = float(rng.choice([0.0, 0.0, 0.1, 0.25, 0.5]))
+        seed_, off = int(rng.integers(0, 2**63)), int(rng.integers(0, 2**40))
+        cases.append((dt, int(rng.integers(1, 4)), S_q, S_kv, D_qk, D_v, causal, p, seed_, off))
+    return cases
+
+
+RANDOM = _random_cases()
+
+
+@pytest.mark.parametrize("case", RANDOM, ids=[f"r{i}-" + "-".join(map(str, e[:8])) for i, e in enumerate(RANDOM)])
+def test_random_shapes(pkg, O, case):
+    dt, B, S_q, S_kv, D_qk, D_v, causal, p, seed_, off = case
+    c = Cfg(f"rand_{dt}_{B}x{S_q}x{S_kv}_{D_qk}_{D_v}", dt, B, S_q, S_kv, D_qk, D_v, causal, p,
+            D_qk ** -0.5, seed=seed_, offset=off)
+    run_and_check(pkg, O, c, fp32_sum_allowance=True)
+
+
 def test_unaligned_pointers_take_scalar_path(pkg, O):
     """Views starting 2 elements into a buffer are not 16-byte aligned: the
     kernels fall back to element loads/stores and must agree."""
