@@ -54,12 +54,17 @@ struct FwdDmaCfg {
     static constexpr int NSTAGE = 2 * 3 * STAGE <= 160 * 1024 ? 3 : 2;
     static constexpr size_t LDS_BYTES = NSTAGE * (size_t)STAGE;
     static_assert(2 * LDS_BYTES <= 160 * 1024, "two workgroups per CU in gfx950 LDS");
+    // waves per SIMD: three when three workgroups' LDS fits, D <= 64 and no
+    // dropout (the register footprint then stays under 168 without spills)
+    template <bool DROP>
+    static constexpr int wpe() { return (!DROP && DQK <= 64 && DV <= 64 && 3 * LDS_BYTES <= 160 * 1024) ? 3 : 2; }
     // every read offset (tile + rows) fits the 16-bit DS immediate
     static_assert(KB + VB <= 65536, "LDS immediates");
 };
 
 template <int DQK, int DV, bool CAUSAL, bool DROP>
-__global__ __launch_bounds__((FwdDmaCfg<DQK, DV>::NT)) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__((FwdDmaCfg<DQK, DV>::NT))
+__attribute__((amdgpu_waves_per_eu(FwdDmaCfg<DQK, DV>::template wpe<DROP>(), FwdDmaCfg<DQK, DV>::template wpe<DROP>())))
 void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
     using Cfg = FwdDmaCfg<DQK, DV>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV, NW = Cfg::NW, NSTAGE = Cfg::NSTAGE;
