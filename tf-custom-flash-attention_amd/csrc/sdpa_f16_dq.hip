@@ -32,10 +32,14 @@ struct DqDmaCfg {
     static constexpr int LK = DQK / 8, LV = DV / 8;
     static constexpr int KB = BN * DQK * 2, VB = BN * DV * 2, STAGE = KB + VB;
     static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+    // waves per SIMD: three for D <= 64 without dropout (registers under 168)
+    template <bool DROP>
+    static constexpr int wpe() { return (!DROP && DQK <= 64 && DV <= 64 && 3 * LDS_BYTES <= 160 * 1024) ? 3 : 2; }
 };
 
 template <int DQK, int DV, bool CAUSAL, bool DROP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(DqDmaCfg<DQK, DV>::template wpe<DROP>(), DqDmaCfg<DQK, DV>::template wpe<DROP>())))
 void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
     using Cfg = DqDmaCfg<DQK, DV>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV;
