@@ -11,7 +11,8 @@
 //   S^T = K Q^T, online softmax over keys in the log2 domain,
 //   O^T += V^T P~^T with P~ taken from the S accumulator straight into the B
 //   operand of the PV MFMA.
-// Four waves (128 queries) per workgroup, two workgroups per CU, stream
+// Four waves (128 queries) per workgroup, two workgroups per CU (three at
+// D <= 64 without dropout), stream
 // blocks of 64 keys through an LDS ring (three deep when it fits, else two),
 // one barrier per block: each block's copy is issued one or two steps before
 // it is read.
@@ -44,7 +45,7 @@ template <int DQK, int DV>
 struct FwdDmaCfg {
     // NW waves of 32 queries each; K/V blocks of BN keys in an NSTAGE-deep
     // LDS ring (the copy of block n + NSTAGE - 1 is issued at step n).  Two
-    // workgroups share a CU, so the two waves on a SIMD belong to different
+    // or three workgroups share a CU, so the waves on a SIMD belong to different
     // workgroups and never wait at each other's barriers (a workgroup of
     // eight waves, two per SIMD, measured slower: each step the older wave
     // finishes first and the other then runs alone).
