@@ -146,8 +146,11 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
     // (left to itself the compiler reads each operand just before its MFMA
     // and waits out the whole LDS latency every time); the transposed reads
     // for dQ go out before the element-wise work and land during it.
-    constexpr int NK = DQK / 16, NV = DV / 16, RD = SDPA_RD;
+    constexpr int NK = DQK / 16, NV = DV / 16, RD_FULL = SDPA_RD;
     auto sub = [&]<bool PART>(uint32_t kbase, int k0, int t) {
+        // masked sub-tiles read one operand ahead: their mask code needs the
+        // registers (RD ahead spills at D = 128)
+        constexpr int RD = PART ? 1 : RD_FULL;
         const uint32_t aK = kbase + swK.row, aV = kbase + Cfg::KB + swV.row;
         const uint32_t aK0 = kbase + swK.tr0, aK1 = kbase + swK.tr1;
         auto rd = [&](int i) { return i < NK ? lds_row<LK>(aK, i, 32 * t) : lds_row<LV>(aV, i - NK, 32 * t); };
