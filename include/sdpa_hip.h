@@ -25,7 +25,10 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#include <hip/hip_runtime_api.h>
+/* The stream handle type of the HIP runtime (hip/hip_runtime_api.h declares
+ * the same typedef), so that a host binding written in plain C or C++ needs
+ * neither the HIP headers nor a HIP platform macro to include this file. */
+typedef struct ihipStream_t* hipStream_t;
 
 #ifdef __cplusplus
 extern "C" {

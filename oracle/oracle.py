@@ -49,13 +49,17 @@ def lib():
         L.oracle_float_to_half.argtypes = [_flt]
         L.oracle_half_to_float.restype = _flt
         L.oracle_half_to_float.argtypes = [ctypes.c_uint16]
+        L.oracle_float_to_half_n.restype = None
+        L.oracle_float_to_half_n.argtypes = [_vp, _vp, ctypes.c_size_t]
+        L.oracle_half_to_float_n.restype = None
+        L.oracle_half_to_float_n.argtypes = [_vp, _vp, ctypes.c_size_t]
         L.oracle_sdpa_fwd.restype = _int
         L.oracle_sdpa_fwd.argtypes = [_int, _vp, _vp, _vp, _vp, _vp, _int, _int, _int, _int, _int,
-                                      _int, _flt, _flt, _u64, _u64, _int, _int, _int, _int]
+                                      _int, _flt, _flt, _u64, _u64, _int, _int, _int, _int, _int]
         L.oracle_sdpa_bwd.restype = _int
         L.oracle_sdpa_bwd.argtypes = [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _int,
                                       _int, _int, _int, _int, _int, _flt, _flt, _u64, _u64, _int,
-                                      _int, _int, _int, _int]
+                                      _int, _int, _int, _int, _int, _int, _int, _int]
         _lib = L
     return _lib
 
@@ -81,6 +85,22 @@ def keep_mask(B: int, S_q: int, S_kv: int, dropout: float, seed: int, offset: in
     return out
 
 
+def float_to_half_bits(x: np.ndarray) -> np.ndarray:
+    """uint16 bit patterns of the oracle's float -> half conversion (RNE)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_float_to_half_n(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def half_bits_to_float(h: np.ndarray) -> np.ndarray:
+    """float32 values of the oracle's half -> float conversion."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_half_to_float_n(h.ctypes.data, out.ctypes.data, h.size)
+    return out
+
+
 def _dtype_code(a: np.ndarray) -> int:
     if a.dtype == np.float32:
         return 0
@@ -93,11 +113,21 @@ def _c(a: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(a)
 
 
+def _span(sp):
+    """(begin, end[, step]) -> three ints; None -> everything."""
+    if sp is None:
+        return (0, -1, 1)
+    sp = tuple(int(x) for x in sp)
+    return sp + (1,) if len(sp) == 2 else sp
+
+
 def sdpa_fwd(q, k, v, *, scale=1.0, dropout=0.0, causal_mask=False, seed=0, offset=0,
              gpu_gates=True, nthreads=None, rows=None):
     """Reference forward (sdpa_cpu.cc:213-320). Returns (o [B,S_q,D_v] in q.dtype, stats f32 [B,S_q]).
 
-    rows=(i0, i1) computes only query rows [i0, i1) (a timing sample)."""
+    rows=(i0, i1[, step]) computes only query rows i0, i0 + step, ... < i1
+    (a timing sample, or a cheap check of every batch); other rows of the
+    outputs are left uninitialised."""
     q, k, v = _c(q), _c(k), _c(v)
     assert q.dtype == k.dtype == v.dtype
     B, S_q, D_qk = q.shape
@@ -108,14 +138,19 @@ def sdpa_fwd(q, k, v, *, scale=1.0, dropout=0.0, causal_mask=False, seed=0, offs
                                o.ctypes.data, stats.ctypes.data, B, S_q, S_kv, D_qk, D_v,
                                int(bool(causal_mask)), float(dropout), float(scale), int(seed),
                                int(offset), int(bool(gpu_gates)), nthreads or default_threads(),
-                               *(rows or (0, -1)))
+                               *_span(rows))
     assert rc == 0
     return o, stats
 
 
 def sdpa_bwd(q, k, v, o, stats, d_o, *, scale=1.0, dropout=0.0, causal_mask=False, seed=0,
-             offset=0, gpu_gates=True, accumulate_kv_in_t=False, nthreads=None, rows=None):
-    """Reference backward (sdpa_cpu.cc:322-457). Returns (dq, dk, dv) in q.dtype."""
+             offset=0, gpu_gates=True, accumulate_kv_in_t=False, nthreads=None, rows=None,
+             keys=None):
+    """Reference backward (sdpa_cpu.cc:322-457). Returns (dq, dk, dv) in q.dtype.
+
+    rows / keys = (begin, end[, step]) restrict the (query, key) pairs that
+    are visited: dq of a row is complete only with every key visited, dk / dv
+    of a key only with every row visited."""
     q, k, v, o, d_o = _c(q), _c(k), _c(v), _c(o), _c(d_o)
     stats = np.ascontiguousarray(stats, dtype=np.float32)
     B, S_q, D_qk = q.shape
@@ -128,7 +163,7 @@ def sdpa_bwd(q, k, v, o, stats, d_o, *, scale=1.0, dropout=0.0, causal_mask=Fals
                                dk.ctypes.data, dv.ctypes.data, B, S_q, S_kv, D_qk, D_v,
                                int(bool(causal_mask)), float(dropout), float(scale), int(seed),
                                int(offset), int(bool(gpu_gates)), int(bool(accumulate_kv_in_t)),
-                               nthreads or default_threads(), *(rows or (0, -1)))
+                               nthreads or default_threads(), *_span(rows), *_span(keys))
     assert rc == 0
     return dq, dk, dv
 

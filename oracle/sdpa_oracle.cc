@@ -29,7 +29,12 @@
 //
 // Parity status: the RNG, thresholds, epsilons and loop structure are pinned
 // by the tests in tests/test_oracle.py (closed-form known answers, float64
-// brute-force attention, finite differences).  The ulp behaviour of the
+// brute-force attention, finite differences).  The F16 semantics are pinned
+// by tests/test_oracle_fp16.py: both converters against numpy's binary16
+// (half -> float over all 65,536 patterns, float -> half on every rounding
+// tie; a one-off run over all 2^32 float patterns also agreed), and closed
+// forms for the half-rounded products and the half read-modify-write of
+// dK / dV that the unrounded variants fail.  The ulp behaviour of the
 // reference's Eigen::numext::exp/log is not available here (TensorFlow's Eigen
 // is not vendored), so results agree with the reference to rounding only:
 // parity unpinned at the ulp level, absorbed by the stated tolerances.
@@ -135,16 +140,22 @@ struct Shape {
     int B, S_q, S_kv, D_qk, D_v;
 };
 
+// Indices begin, begin + step, ... below end (a subset of query rows or keys
+// to compute; the full range is {0, S, 1}).
+struct Span {
+    int begin, end, step;
+};
+
 template <typename T>
 void fwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
                const typename T::storage* K, const typename T::storage* V,
                typename T::storage* Out, float* stats, bool causal, float dropout, float scale,
-               uint64_t seed, uint64_t offset, bool gpu_gates, int row_begin, int row_end) {
+               uint64_t seed, uint64_t offset, bool gpu_gates, const Span& rows) {
     const bool use_dropout = gpu_gates ? (dropout > kEps) : (dropout > 0.0f);
     const float dp_inverse_scale = use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
     std::vector<float> acc(s.D_v);
     const size_t qb = (size_t)b * s.S_q, kb = (size_t)b * s.S_kv;
-    for (int i = row_begin; i < row_end; ++i) {
+    for (int i = rows.begin; i < rows.end; i += rows.step) {
         float m_i = kNegInf;
         float l_i = 0.0f;
         std::fill(acc.begin(), acc.end(), 0.0f);
@@ -184,7 +195,8 @@ void bwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
                const typename T::storage* Out, const float* Stats,
                const typename T::storage* dO, typename T::storage* dQ, typename T::storage* dK,
                typename T::storage* dV, bool causal, float dropout, float scale, uint64_t seed,
-               uint64_t offset, bool gpu_gates, bool accumulate_kv_in_t, int row_begin, int row_end) {
+               uint64_t offset, bool gpu_gates, bool accumulate_kv_in_t, const Span& rows,
+               const Span& keys) {
     const bool use_dropout = gpu_gates ? (dropout > kEps) : (dropout > 0.0f);
     const float dp_inverse_scale = use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
     const size_t qb = (size_t)b * s.S_q, kb = (size_t)b * s.S_kv;
@@ -193,13 +205,13 @@ void bwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
     // (sdpa_bwd.cu.cc:49-56,159-170) and are rounded once at the end.
     std::vector<float> dk_acc((size_t)s.S_kv * s.D_qk, 0.0f), dv_acc((size_t)s.S_kv * s.D_v, 0.0f);
     std::vector<float> dq_acc(s.D_qk);
-    for (int i = row_begin; i < row_end; ++i) {
+    for (int i = rows.begin; i < rows.end; i += rows.step) {
         const float stats_val = Stats[qb + i];
         float D_i = 0.0f;  // sdpa_cpu.cc:360-364
         for (int k = 0; k < s.D_v; ++k)
             D_i += T::mul(T::load(dO, (qb + i) * s.D_v + k), T::load(Out, (qb + i) * s.D_v + k));
         std::fill(dq_acc.begin(), dq_acc.end(), 0.0f);
-        for (int j = 0; j < s.S_kv; ++j) {
+        for (int j = keys.begin; j < keys.end; j += keys.step) {
             if (causal && j > i) continue;
             float score = 0.0f;
             for (int k = 0; k < s.D_qk; ++k)
@@ -242,6 +254,14 @@ void bwd_batch(int64_t b, const Shape& s, const typename T::storage* Q,
     }
     for (size_t x = 0; x < (size_t)s.S_kv * s.D_qk; ++x) T::store(dK, kb * s.D_qk + x, dk_acc[x]);
     for (size_t x = 0; x < (size_t)s.S_kv * s.D_v; ++x) T::store(dV, kb * s.D_v + x, dv_acc[x]);
+}
+
+// Span of indices from (begin, end, step) arguments: end < 0 means n, a
+// non-positive step means 1.
+Span make_span(int begin, int end, int step, int n) {
+    if (end < 0 || end > n) end = n;
+    if (begin < 0) begin = 0;
+    return Span{begin, end, step > 0 ? step : 1};
 }
 
 // Shard [0, B) over `nthreads` threads in contiguous ranges (the reference uses
@@ -290,28 +310,35 @@ void oracle_keep_mask(int B, int S_q, int S_kv, float dropout, uint64_t seed, ui
 uint16_t oracle_float_to_half(float f) { return float_to_half(f); }
 float oracle_half_to_float(uint16_t h) { return half_to_float(h); }
 
+// Array forms of the two converters (for exhaustive checks from Python).
+void oracle_float_to_half_n(const float* in, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = float_to_half(in[i]);
+}
+void oracle_half_to_float_n(const uint16_t* in, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = half_to_float(in[i]);
+}
+
 // dtype: 0 = fp32, 1 = fp16 (faithful Eigen::half semantics).
-// Query rows [row_begin, row_end) of every batch are computed (row_end < 0:
-// all rows); the others are left untouched.  A row range is only used to
-// time a bounded sample of a large workload.
+// Query rows row_begin, row_begin + row_step, ... below row_end of every batch
+// are computed (row_end < 0: all rows); the others are left untouched.  A row
+// subset is used to time a bounded sample of a large workload and to check
+// every batch of a large configuration on a few rows.
 int oracle_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* stats,
                     int B, int S_q, int S_kv, int D_qk, int D_v, int causal, float dropout,
                     float scale, uint64_t seed, uint64_t offset, int gpu_gates, int nthreads,
-                    int row_begin, int row_end) {
+                    int row_begin, int row_end, int row_step) {
     const Shape s{B, S_q, S_kv, D_qk, D_v};
-    if (row_end < 0 || row_end > S_q) row_end = S_q;
-    if (row_begin < 0) row_begin = 0;
+    const Span rows = make_span(row_begin, row_end, row_step, S_q);
     if (dtype == 0) {
         parallel_over_batch(B, nthreads, [&](int64_t b) {
             fwd_batch<F32>(b, s, (const float*)q, (const float*)k, (const float*)v, (float*)o, stats,
-                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0, row_begin,
-                           row_end);
+                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0, rows);
         });
     } else if (dtype == 1) {
         parallel_over_batch(B, nthreads, [&](int64_t b) {
             fwd_batch<F16>(b, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                            (uint16_t*)o, stats, causal != 0, dropout, scale, seed, offset,
-                           gpu_gates != 0, row_begin, row_end);
+                           gpu_gates != 0, rows);
         });
     } else {
         return 1;
@@ -321,27 +348,31 @@ int oracle_sdpa_fwd(int dtype, const void* q, const void* k, const void* v, void
 
 // accumulate_kv_in_t: 1 reproduces the reference CPU kernel's per-row rounding of
 // dK/dV to T; 0 accumulates them in fp32 (as the reference GPU kernels do).
+// The (i, j) pairs visited are the query rows of (row_begin, row_end,
+// row_step) times the keys of (key_begin, key_end, key_step): dQ of a row is
+// complete when every key is visited, dK / dV of a key when every row is.
 int oracle_sdpa_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
                     const float* stats, const void* d_o, void* dq, void* dk, void* dv, int B,
                     int S_q, int S_kv, int D_qk, int D_v, int causal, float dropout, float scale,
                     uint64_t seed, uint64_t offset, int gpu_gates, int accumulate_kv_in_t,
-                    int nthreads, int row_begin, int row_end) {
+                    int nthreads, int row_begin, int row_end, int row_step, int key_begin,
+                    int key_end, int key_step) {
     const Shape s{B, S_q, S_kv, D_qk, D_v};
-    if (row_end < 0 || row_end > S_q) row_end = S_q;
-    if (row_begin < 0) row_begin = 0;
+    const Span rows = make_span(row_begin, row_end, row_step, S_q);
+    const Span keys = make_span(key_begin, key_end, key_step, S_kv);
     if (dtype == 0) {
         parallel_over_batch(B, nthreads, [&](int64_t b) {
             bwd_batch<F32>(b, s, (const float*)q, (const float*)k, (const float*)v, (const float*)o,
                            stats, (const float*)d_o, (float*)dq, (float*)dk, (float*)dv,
-                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0, false,
-                           row_begin, row_end);
+                           causal != 0, dropout, scale, seed, offset, gpu_gates != 0, false, rows,
+                           keys);
         });
     } else if (dtype == 1) {
         parallel_over_batch(B, nthreads, [&](int64_t b) {
             bwd_batch<F16>(b, s, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                            (const uint16_t*)o, stats, (const uint16_t*)d_o, (uint16_t*)dq,
                            (uint16_t*)dk, (uint16_t*)dv, causal != 0, dropout, scale, seed, offset,
-                           gpu_gates != 0, accumulate_kv_in_t != 0, row_begin, row_end);
+                           gpu_gates != 0, accumulate_kv_in_t != 0, rows, keys);
         });
     } else {
         return 1;

@@ -109,3 +109,86 @@ def test_headline_key_batch_subset(pkg, O):
         assert np.array_equal(got, ref)
         # drop rate close to p on 16.7M samples
         assert abs(1.0 - got.mean() - p) < 1e-3
+
+
+# ---------------------------------------------------------------------------
+# Causal runs at the DMA kernels' own widths (D_qk = D_v = D): the masked
+# diagonal sub-tiles and the causal branches of every kernel apply the hash.
+# ---------------------------------------------------------------------------
+def _masks_through_kernels(pkg, B, S, p, seed, off, D, causal=True, dt=torch.float16):
+    """(forward, dK/dV, dQ) keep masks read back through the production
+    kernels at width D; entries the causal mask hides read as 0.
+
+      forward : q = 0, V[j, d] = [j == d + D t]          -> o[i, d] > 0
+      dK/dV   : q = 0, dO[i, d] = [i == d + D t]         -> dV[j, d] > 0
+      dQ      : q = 0, K[j, d] = [j == d + D t], V = dO = e_0, and O = 0
+                passed to the backward, so delta = 0 and
+                dS(i, j) = P keep / (1 - p) > 0 exactly for kept elements
+                                                          -> dQ[i, d] > 0
+    (with the real O, a row whose elements are all kept has dS = 0 for every
+    element, which a causal row 0 often is)."""
+    shape = (B, S, D)
+    zeros = lambda: torch.zeros(shape, dtype=dt, device=DEV)
+    kw = dict(dropout=p, scale=1.0, causal_mask=causal)
+    q = zeros()
+    k_rand = torch.randn(shape, device=DEV).to(dt)
+    v_rand = torch.randn(shape, device=DEV).to(dt)
+    fwd = np.zeros((B, S, S), np.uint8)
+    dkdv = np.zeros_like(fwd)
+    dq = np.zeros_like(fwd)
+    o_r, s_r = pkg.sdpa(q, k_rand, v_rand, seed, off, **kw)
+    e0 = zeros()
+    e0[:, :, 0] = 1
+    for t in range((S + D - 1) // D):
+        idx = torch.arange(D * t, min(S, D * t + D), device=DEV)
+        n = len(idx)
+        onehot = zeros()
+        onehot[:, idx, idx - D * t] = 1
+        o, _ = pkg.sdpa(q, k_rand, onehot, seed, off, **kw)
+        fwd[:, :, D * t:D * t + n] = (o[:, :, :n] > 0).cpu().numpy()
+        _, _, dv = pkg.sdpa_grad(q, k_rand, v_rand, o_r, s_r, onehot, seed, off, **kw)
+        dkdv[:, D * t:D * t + n, :] = (dv[:, :, :n] > 0).permute(0, 2, 1).cpu().numpy()
+        _, s1 = pkg.sdpa(q, onehot, e0, seed, off, **kw)
+        g, _, _ = pkg.sdpa_grad(q, onehot, e0, zeros(), s1, e0, seed, off, **kw)
+        dq[:, :, D * t:D * t + n] = (g[:, :, :n] > 0).cpu().numpy()
+    torch.cuda.synchronize()
+    return fwd, dkdv, dq
+
+
+def _expected(O, B, S, p, seed, off, causal=True):
+    ref = O.keep_mask(B, S, S, p, seed, off)
+    if causal:
+        ref &= np.tril(np.ones((S, S), np.uint8))[None]
+    return ref
+
+
+CAUSAL_CASES = [
+    # (B, S, p, seed, offset, D)
+    (2, 300, 0.1, 7, 0, 128),
+    (2, 300, 0.2, 42, 1000, 64),
+    (1, 333, 0.5, 99, 2**40 + 3, 128),
+    (3, 200, 0.3, 5, 6, 32),
+    (2, 130, 0.25, 11, 12, 64),
+]
+
+
+@pytest.mark.parametrize("case", CAUSAL_CASES, ids=[f"B{c[0]}_S{c[1]}_p{c[2]}_D{c[5]}" for c in CAUSAL_CASES])
+def test_causal_masks_through_kernels(pkg, O, case):
+    B, S, p, seed, off, D = case
+    print(f"[case] causal mask B={B} S={S} p={p} D={D}", flush=True)
+    ref = _expected(O, B, S, p, seed, off)
+    for name, got in zip(("fwd", "dkdv", "dq"), _masks_through_kernels(pkg, B, S, p, seed, off, D)):
+        assert np.array_equal(got, ref), (name, int((got != ref).sum()))
+
+
+@pytest.mark.parametrize("b", [0, 127])
+def test_headline_masks_through_kernels(pkg, O, b):
+    """c4's own instantiation (fp16, D_qk = D_v = 128, causal, p = 0.1,
+    seed 7, S = 4096) for batches 0 and 127 of B = 128: batch b of the full
+    run is batch 0 of a run with offset + b S^2 (the counter is linear)."""
+    S, p, seed = 4096, 0.1, 7
+    off = b * S * S
+    print(f"[case] headline mask batch {b}", flush=True)
+    ref = _expected(O, 1, S, p, seed, off)
+    for name, got in zip(("fwd", "dkdv", "dq"), _masks_through_kernels(pkg, 1, S, p, seed, off, 128)):
+        assert np.array_equal(got, ref), (name, int((got != ref).sum()))

@@ -24,7 +24,43 @@ def _np(t):
     return t.detach().cpu().numpy()
 
 
-def run_and_check(pkg, O, c: Cfg, inputs=None, check_faithful=False, fp32_sum_allowance=False):
+def subset_rows(S: int, head: int, step: int = 61):
+    """The first `head` indices, then every `step`-th one (a step prime to the
+    64 / 128-row tiles, so the checked rows fall at every position of a tile)."""
+    return [(0, min(head, S), 1)] + ([(head, S, step)] if S > head else [])
+
+
+def check_all_batches(O, c: Cfg, inputs, outputs):
+    """Every batch of a large configuration against the oracle on a subset:
+    o, stats and dQ on the first query rows (cheap under the causal mask) and
+    every 61st row after them; dK and dV on the last keys (cheap under the
+    causal mask) and every 61st key before them.  The dropout counter is
+    global, so the oracle runs on the whole batch range with the config's own
+    offset; a tile mapped to the wrong batch or position fails here."""
+    q, k, v, d_o = inputs
+    o_h, s_h, dq_h, dk_h, dv_h = outputs
+    okw = oracle_kw(c, 0)
+    head = 128 if c.causal else 32
+    errs = {"o": 0.0, "stats": 0.0, "dq": 0.0, "dk": 0.0, "dv": 0.0}
+    for r in subset_rows(c.S_q, head):
+        sl = slice(*r)
+        o_ref, s_ref = O.sdpa_fwd_gate(q, k, v, rows=r, **okw)
+        errs["o"] = max(errs["o"], maxabs(o_h[:, sl], o_ref[:, sl]))
+        errs["stats"] = max(errs["stats"], maxabs(s_h[:, sl], s_ref[:, sl]))
+        dq_ref, _, _ = O.sdpa_bwd_gate(q, k, v, o_h, s_h, d_o, rows=r, **okw)
+        errs["dq"] = max(errs["dq"], maxabs(dq_h[:, sl], dq_ref[:, sl]))
+    tail = min(head, c.S_kv)
+    for r in [(c.S_kv - tail, c.S_kv, 1), (0, c.S_kv - tail, 61)]:
+        if r[0] >= r[1]:
+            continue
+        sl = slice(*r)
+        _, dk_ref, dv_ref = O.sdpa_bwd_gate(q, k, v, o_h, s_h, d_o, keys=r, **okw)
+        errs["dk"] = max(errs["dk"], maxabs(dk_h[:, sl], dk_ref[:, sl]))
+        errs["dv"] = max(errs["dv"], maxabs(dv_h[:, sl], dv_ref[:, sl]))
+    return errs
+
+
+def run_and_check(pkg, O, c: Cfg, inputs=None, fp32_sum_allowance=False):
     """fp32_sum_allowance: for shapes beyond the BASELINE configs, an fp32
     gradient may also differ from the fp32 oracle by the rounding of two
     different summation orders over L = max(S_q, S_kv) terms, bounded here by
@@ -64,6 +100,12 @@ def run_and_check(pkg, O, c: Cfg, inputs=None, check_faithful=False, fp32_sum_al
             errs[name] = max(errs[name], maxabs(sel(got), ref))
             refmax[name] = max(refmax[name], float(np.abs(ref.astype(np.float64)).max()) if ref.size else 0.0)
     print(f"[errs] {c.name}: " + " ".join(f"{k}={v:.3e}" for k, v in errs.items()), flush=True)
+    if c.check_batches:
+        sub = check_all_batches(O, c, (q, k, v, d_o), (o_h, s_h, dq_h, dk_h, dv_h))
+        print(f"[errs] {c.name} all batches: " + " ".join(f"{k}={v:.3e}" for k, v in sub.items()),
+              flush=True)
+        for name, e in sub.items():
+            errs[name] = max(errs[name], e)
     assert errs["o"] <= tol["o"], errs
     assert errs["stats"] <= tol["stats"], errs
     for name in ("dq", "dk", "dv"):
@@ -117,6 +159,64 @@ def test_edge_shapes(pkg, O, case):
     run_and_check(pkg, O, c, fp32_sum_allowance=True)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("p", [0.0, 0.1])
+def test_fp16_large_outputs_few_keys(pkg, O, D, p):
+    """Causal rows that average only a few keys, with V scaled by 6 so that
+    many outputs of rows 1-8 lie in [4, 8), where one fp16 ulp (3.9e-3) is
+    larger than the 2e-3 gate.  The kernel's fp16 o is compared with the
+    oracle's o before its final cast to fp16 (the fp32 value the reference
+    rounds, sdpa_cpu.cc:308), so the error holds the kernel's own output
+    rounding (at most half an ulp) plus its arithmetic error.
+
+    Rows 0-63 (at most 64 visible keys; the forward feeds P~ to the PV
+    product as two fp16 parts there):
+      |o - o_ref| <= ulp(o_ref) / 2 + 1e-5     (o is o_ref correctly rounded)
+      |o - o_ref| <= 2e-3 where |o_ref| < 8    (north_star's o gate; from 8 on
+                                                 half an ulp alone exceeds it)
+    Rows 64 on (fp16 P~ in the PV product): the error is bounded by the
+    rounding of each P_j to fp16, |dP_j| <= 2^-11 P_j, i.e.
+      |o - o_ref| <= ulp(o_ref) / 2 + 2^-11 sum_j P~_j |v_j| / l + 1e-4
+    with P_j / l = exp(scale q.k_j - stats) from the oracle's statistics (the
+    1e-4 covers P~ below fp16's normal range).  With V ~ N(0, 36) that bound
+    reaches ~1.2e-3 in peaked rows, so the 2e-3 gate is not asserted there;
+    the BASELINE configurations (V ~ N(0, 1)) meet it in every row."""
+    c = Cfg(f"margin_d{D}_p{p}", "f16", 4, 256, 256, D, D, True, p, D ** -0.5, 7, 0)
+    q, k, v, _ = make_inputs(c)
+    v = (v.astype(np.float32) * 6).astype(np.float16)
+    print(f"[case] {c.name}", flush=True)
+    o, s = pkg.sdpa(_t(q), _t(k), _t(v), c.seed, c.offset, dropout=p, scale=c.scale,
+                    causal_mask=True)
+    torch.cuda.synchronize()
+    o_h = _np(o).astype(np.float64)
+    f32 = lambda a: a.astype(np.float32)
+    o_ref, s_ref = O.sdpa_fwd(f32(q), f32(k), f32(v), **oracle_kw(c))
+    o_ref = o_ref.astype(np.float64)
+    few = slice(0, 64)
+    big = (np.abs(o_ref[:, 1:9]) >= 4) & (np.abs(o_ref[:, 1:9]) < 8)
+    assert big.sum() > 100, int(big.sum())  # the case under test exists
+    err = np.abs(o_h - o_ref)
+    half_ulp = np.spacing(np.abs(o_ref).astype(np.float16)).astype(np.float64) / 2
+    # 2^-11 sum_j P~_j |v_j| / l per output element (float64, dense)
+    S = c.S_q
+    sc = c.scale * np.einsum("bid,bjd->bij", q.astype(np.float64), k.astype(np.float64))
+    sc = np.where(np.tril(np.ones((S, S), bool))[None], sc, -np.inf)
+    pl = np.exp(sc - s_ref.astype(np.float64)[..., None])
+    if p > 0:
+        pl = pl * O.keep_mask(c.B, S, S, p, c.seed, c.offset) / (1.0 - p)
+    p16 = 2.0 ** -11 * np.einsum("bij,bjd->bid", pl, np.abs(v.astype(np.float64)))
+    excess_few = float((err[:, few] - half_ulp[:, few]).max())
+    gate_few = err[:, few][np.abs(o_ref[:, few]) < 8].max()
+    excess_rest = float((err[:, 64:] - half_ulp[:, 64:] - p16[:, 64:]).max())
+    print(f"[errs] {c.name}: rows<64 max excess over half ulp={excess_few:.2e} max|o-o_ref|(|o|<8)="
+          f"{gate_few:.3e}; rows>=64 max|o-o_ref|={err[:, 64:].max():.3e} excess over the fp16-P bound="
+          f"{excess_rest:.2e}; stats={maxabs(_np(s), s_ref):.2e}", flush=True)
+    assert excess_few <= 1e-5
+    assert gate_few <= 2e-3
+    assert excess_rest <= 1e-4
+    assert maxabs(_np(s), s_ref) <= TOL["f16"]["stats"]
+
+
 def _random_cases(n=24, seed=2024):
     """Seeded shapes beyond the hand-picked ones: any D in 1..128 (both kernel
     families), ragged sequence lengths, cross attention, dropout rates, large
@@ -150,7 +250,8 @@ def test_random_shapes(pkg, O, case):
 
 def test_unaligned_pointers_take_scalar_path(pkg, O):
     """Views starting 2 elements into a buffer are not 16-byte aligned: the
-    kernels fall back to element loads/stores and must agree."""
+    register-staged kernels (element loads / stores) run instead of the
+    DMA-fed ones, and both pass the fp16 gates against the oracle."""
     c = Cfg("unaligned", "f16", 2, 70, 70, 64, 64, True, 0.2, 0.125, 3, 9)
     q, k, v, d_o = make_inputs(c)
     def shifted(a):
@@ -159,17 +260,17 @@ def test_unaligned_pointers_take_scalar_path(pkg, O):
         view.copy_(_t(a))
         return view
     kw = dict(dropout=c.dropout, scale=c.scale, causal_mask=c.causal)
-    o1, s1 = pkg.sdpa(shifted(q), shifted(k), shifted(v), c.seed, c.offset, **kw)
-    o2, s2 = pkg.sdpa(_t(q), _t(k), _t(v), c.seed, c.offset, **kw)
-    torch.cuda.synchronize()
-    assert maxabs(_np(o1), _np(o2)) <= 1e-3
-    assert maxabs(_np(s1), _np(s2)) <= 1e-5
-    g1 = pkg.sdpa_grad(shifted(q), shifted(k), shifted(v), shifted(_np(o2)), s2, shifted(d_o),
-                       c.seed, c.offset, **kw)
-    g2 = pkg.sdpa_grad(_t(q), _t(k), _t(v), o2, s2, _t(d_o), c.seed, c.offset, **kw)
-    torch.cuda.synchronize()
-    for a, b in zip(g1, g2):
-        assert maxabs(_np(a), _np(b)) <= 5e-3
+    okw = oracle_kw(c)
+    o_ref, s_ref = O.sdpa_fwd_gate(q, k, v, **okw)
+    for make in (shifted, _t):
+        o, s = pkg.sdpa(make(q), make(k), make(v), c.seed, c.offset, **kw)
+        g = pkg.sdpa_grad(make(q), make(k), make(v), make(_np(o)), s, make(d_o), c.seed, c.offset, **kw)
+        torch.cuda.synchronize()
+        assert maxabs(_np(o), o_ref) <= TOL["f16"]["o"]
+        assert maxabs(_np(s), s_ref) <= TOL["f16"]["stats"]
+        g_ref = O.sdpa_bwd_gate(q, k, v, _np(o), _np(s), d_o, **okw)
+        for a, r in zip(g, g_ref):
+            assert maxabs(_np(a), r) <= TOL["f16"]["grad"]
 
 
 @pytest.mark.parametrize("dt", ["f16", "f32"])

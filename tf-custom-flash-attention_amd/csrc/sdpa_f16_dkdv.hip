@@ -557,15 +557,12 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
         for (int ks = 0; ks < DV / 16; ++ks)
             vreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Vb, my_k, S_kv, 16 * ks + 8 * hh, D_v, D_v));
-        // With dropout V is held as V / (1 - p) (rounded to fp16), so the MFMA
-        // yields dP / (1 - p) directly.
-        if constexpr (DROP) {
-            const float ksc = p.c.keep_scale;
-#pragma unroll
-            for (int ks = 0; ks < DV / 16; ++ks)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) vreg[ks][e] = (half_t)((float)vreg[ks][e] * ksc);
-        }
+        // With dropout the factor 1/(1-p) is taken out of dS: this role forms
+        //   dS' = P (keep ? dP - delta' : -delta'),  delta' = delta / (1/(1-p))
+        // (the reference's D_i / dp_inverse_scale, sdpa/sdpa_cpu.cc:428) and
+        // dK is stored with scale / (1-p).  Each block's delta row is
+        // rewritten as delta' in LDS once, by the wave that copies it.
+        const float ksc = p.c.keep_scale;
         const float* st2b = p.stats2 + (size_t)b * S_q;
         const float* deltab = p.delta + (size_t)b * S_q;
         TileDma<BQ, LQ, 4> qd;
@@ -591,10 +588,10 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
         for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};
 
-        // dS of one sub-tile from dP' (dP / (1 - p)), delta and the P role's x.
+        // dS' of one sub-tile from dP, delta' and the P role's x.
         auto elem = [&](const floatx16& dpacc, const floatx4 (&de4)[4], const half8& xv0, const half8& xv1,
                         half8& ds0, half8& ds1) {
-            // dS = P (keep ? dP' - delta : -delta) = max(x, 0) dP' - |x| delta
+            // dS' = P (keep ? dP - delta' : -delta') = max(x, 0) dP - |x| delta'
             const half8 xm0 = DROP ? relu_h8(xv0) : xv0;
             const half8 xm1 = DROP ? relu_h8(xv1) : xv1;
             uint32_t wd[8];
@@ -653,6 +650,12 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
                 if (kw == 1)
                     dma4(make_rsrc(deltab + qn, (long long)(S_q - qn) * 4), stn + Cfg::QB + Cfg::OB + BQ * 4, lane * 4);
             }
+            // block n has landed: its delta row becomes delta' (read by this
+            // role from the next step on; the P role never reads it)
+            if (DROP && kw == 1 && n < nsteps) {
+                float* dl = reinterpret_cast<float*>(smem + (n % NSTAGE) * Cfg::STAGE + Cfg::QB + Cfg::OB) + BQ;
+                dl[lane] = dl[lane] / ksc;
+            }
             if (n == 0) continue;
             const int m = n - 1;
             const int q0 = q_top - m * BQ;
@@ -663,8 +666,9 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         }
         if (key_ok) {
             half_t* dKb = static_cast<half_t*>(p.dk) + ((size_t)b * S_kv + my_k) * D_qk;
-            if (D_qk == DQK) store_rows_f16<DQK>(dKb, dkacc, p.c.scale, hh);
-            else store_rows_f16_n<DQK>(dKb, dkacc, p.c.scale, hh, D_qk);
+            const float fk = DROP ? p.c.scale * ksc : p.c.scale;
+            if (D_qk == DQK) store_rows_f16<DQK>(dKb, dkacc, fk, hh);
+            else store_rows_f16_n<DQK>(dKb, dkacc, fk, hh, D_qk);
         }
     }
 }

@@ -146,8 +146,10 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
     // block maximum exceeds the running one by more than 2^kTauF), alpha =
     // exp2(m_run - m_use), P = exp2(s sl2 - m_use), the undropped sum and the
     // dropped, fp16-packed B operands of the PV product.
-    auto softmax_sub = [&](const floatx16& sc, int t, uint64_t st_blk, float& m_use, float& alpha, float& lsum,
-                           half8& pb0, half8& pb1) {
+    // SPLIT: also the fp16 remainders pl = P~ - fp16(P~), so that the PV
+    // product sees P~ to ~2^-22 (rows averaging only a few keys, below).
+    auto softmax_sub = [&]<bool SPLIT>(const floatx16& sc, int t, uint64_t st_blk, float& m_use, float& alpha,
+                                       float& lsum, half8& pb0, half8& pb1, half8& pl0, half8& pl1) {
         // a chain of v_max3 (one per two scores): the opaque steps keep the
         // compiler from re-associating it into a tree of v_max and v_max3,
         // which costs ~1.4 instructions per two scores
@@ -162,7 +164,7 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         m_use = (mx > m_run + kTauF) ? fmaxf(m_run, mx) : m_run;
         alpha = fast_exp2(m_run - m_use);
         const float nm = -m_use;
-        uint32_t w[8];
+        uint32_t w[8], wl[8];
         float lq[4];
         // Hash states walk the lane's keys 32 t + 8 g + e as a chain of adds
         // (opaque to the compiler, which would otherwise fold them into 32
@@ -189,10 +191,20 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
             }
             w[r >> 1] = pack_h2(pq[0], pq[1]);
             w[(r >> 1) + 1] = pack_h2(pq[2], pq[3]);
+            if constexpr (SPLIT) {
+                const half2v h0 = __builtin_bit_cast(half2v, w[r >> 1]);
+                const half2v h1 = __builtin_bit_cast(half2v, w[(r >> 1) + 1]);
+                wl[r >> 1] = pack_h2(pq[0] - (float)h0[0], pq[1] - (float)h0[1]);
+                wl[(r >> 1) + 1] = pack_h2(pq[2] - (float)h1[0], pq[3] - (float)h1[1]);
+            }
         }
         lsum = (lq[0] + lq[1]) + (lq[2] + lq[3]);
         pb0 = half8_of(w[0], w[1], w[2], w[3]);
         pb1 = half8_of(w[4], w[5], w[6], w[7]);
+        if constexpr (SPLIT) {
+            pl0 = half8_of(wl[0], wl[1], wl[2], wl[3]);
+            pl1 = half8_of(wl[4], wl[5], wl[6], wl[7]);
+        }
     };
     // Mask of sub-tile t: keys past S_kv and, causal, keys after the query.
     auto mask_sub = [&](floatx16& sc, int kv0, int t) {
@@ -226,7 +238,13 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
     // The rescale of O by sub-tile 1's new maximum commutes with the pending
     // PV(0) accumulation, so it is applied after R3.
     // mid(k) marks the end of region k (the copy points of the step).
-    auto fwd_step = [&]<bool PART>(int kv0, uint32_t so, auto&& mid) {
+    //
+    // SPLIT (the first key block of a masked step: every row of the wave sees
+    // at most 64 keys): P~ enters the PV product as two fp16 parts, hi + lo.
+    // Over many keys the fp16 rounding of P~ (relative 2^-12) averages out;
+    // over one or two keys it would move o by up to 2^-12 |v|, more than
+    // half an fp16 ulp of o.
+    auto fwd_step = [&]<bool PART, bool SPLIT>(int kv0, uint32_t so, auto&& mid) {
         const bool part0 = PART && (kv0 + 32 > S_kv || (CAUSAL && kv0 + 31 > qw0));
         const bool part1 = PART && (kv0 + 64 > S_kv || (CAUSAL && kv0 + 63 > qw0));
         // Read addresses of this step, formed here (opaque lane terms keep the
@@ -260,8 +278,8 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
                 av0[j][dt] = ld_tr8(tv[dt] + 16 * LV * 16 * j, tv[dt] + 16 * LV * (16 * j + 8));
         if (part0) mask_sub(s0, kv0, 0);
         float mu0, al0, ls0;
-        half8 p00, p01;
-        softmax_sub(s0, 0, st_blk, mu0, al0, ls0, p00, p01);
+        half8 p00, p01, l00, l01;
+        softmax_sub.template operator()<SPLIT>(s0, 0, st_blk, mu0, al0, ls0, p00, p01, l00, l01);
         commit_sub(mu0, al0, ls0);
         mid(2);
         // R3
@@ -269,6 +287,10 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         for (int dt = 0; dt < NDT; ++dt) {
             oacc[dt] = mfma_f16(av0[0][dt], p00, oacc[dt]);
             oacc[dt] = mfma_f16(av0[1][dt], p01, oacc[dt]);
+            if constexpr (SPLIT) {
+                oacc[dt] = mfma_f16(av0[0][dt], l00, oacc[dt]);
+                oacc[dt] = mfma_f16(av0[1][dt], l01, oacc[dt]);
+            }
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
@@ -277,8 +299,8 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
                 av1[j][dt] = ld_tr8(tv[dt] + 16 * LV * (32 + 16 * j), tv[dt] + 16 * LV * (40 + 16 * j));
         if (part1) mask_sub(s1, kv0, 1);
         float mu1, al1, ls1;
-        half8 p10, p11;
-        softmax_sub(s1, 1, st_blk, mu1, al1, ls1, p10, p11);
+        half8 p10, p11, l10, l11;
+        softmax_sub.template operator()<SPLIT>(s1, 1, st_blk, mu1, al1, ls1, p10, p11, l10, l11);
         commit_sub(mu1, al1, ls1);
         mid(3);
         // R4
@@ -286,6 +308,10 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         for (int dt = 0; dt < NDT; ++dt) {
             oacc[dt] = mfma_f16(av1[0][dt], p10, oacc[dt]);
             oacc[dt] = mfma_f16(av1[1][dt], p11, oacc[dt]);
+            if constexpr (SPLIT) {
+                oacc[dt] = mfma_f16(av1[0][dt], l10, oacc[dt]);
+                oacc[dt] = mfma_f16(av1[1][dt], l11, oacc[dt]);
+            }
         }
     };
 
@@ -310,8 +336,10 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
         auto mid = [&](int k) {
             if (cp && wave == k) issue(step + NSTAGE - 1);
         };
-        if (!PART || (live && !(CAUSAL && kv0 > qw0 + 31)))  // else: no visible key in this step
-            fwd_step.template operator()<PART>(kv0, so, mid);
+        if (!PART || (live && !(CAUSAL && kv0 > qw0 + 31))) {  // else: no visible key in this step
+            if (PART && step == 0) fwd_step.template operator()<PART, true>(kv0, so, mid);
+            else fwd_step.template operator()<PART, false>(kv0, so, mid);
+        }
         else if (cp && wave != 0)
             issue(step + NSTAGE - 1);
         if constexpr (DROP) st_blk += (uint64_t)BN * kLcgMul;
