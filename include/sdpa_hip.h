@@ -68,7 +68,8 @@ typedef enum {
     SDPA_ERR_NULL_POINTER = 20,
     SDPA_ERR_DROPOUT_RANGE = 21,
     SDPA_ERR_WORKSPACE = 22,
-    SDPA_ERR_HIP = 23
+    SDPA_ERR_HIP = 23,
+    SDPA_ERR_SCRATCH_LIMIT = 24
 } sdpa_status_t;
 
 /* Message for a status code (static storage, never NULL). */
@@ -131,6 +132,24 @@ int sdpa_hip_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, co
                       size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
                       float scale, float dropout, int causal_mask, uint64_t seed,
                       uint64_t offset, hipStream_t stream);
+
+/* ---- backward that allocates nothing ---------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory or pass a workspace: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  Same arguments and results as
+ * sdpa_hip_bwd without the workspace: the per-query-row values live in a
+ * static device array of SDPA_HIP_NOALLOC_SCRATCH_BYTES per GPU (8 bytes per
+ * query row, so B * S_q <= 2,097,152; larger problems return
+ * SDPA_ERR_SCRATCH_LIMIT).  Calls no hipMalloc / hipFree; its first call on
+ * a device looks up that device's copy of the array (hipGetSymbolAddress).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (different streams, or host threads without ordering) race.          */
+#define SDPA_HIP_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+int sdpa_hip_bwd_noalloc(int dtype, const void* q, const void* k, const void* v, const void* o,
+                         const float* stats, const void* d_o, void* dq, void* dk, void* dv, int B,
+                         int S_q, int S_kv, int D_qk, int D_v, float scale, float dropout,
+                         int causal_mask, uint64_t seed, uint64_t offset, hipStream_t stream);
 
 /* ---- dropout hash (sdpa/sdpa_utils.cuh:13-19, sdpa/sdpa_cpu.cc:198-211) ----
  * Integer form of the reference's predicate (float)(st >> 32) / 2^32 < p:

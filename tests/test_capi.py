@@ -60,7 +60,7 @@ REF_MESSAGES = {
 def test_status_strings(pkg):
     for code, msg in REF_MESSAGES.items():
         assert pkg.status_string(code) == msg
-    for code in range(0, 24):
+    for code in range(0, 25):
         assert pkg.status_string(code)
 
 

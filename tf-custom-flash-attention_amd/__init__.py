@@ -29,7 +29,8 @@ DTYPE_F16 = 1
 # sdpa_status_t (include/sdpa_hip.h)
 SDPA_OK = 0
 SDPA_ERR_HIP = 23
-_ARG_ERRORS = set(range(1, 23))
+SDPA_ERR_SCRATCH_LIMIT = 24
+_ARG_ERRORS = set(range(1, 23)) | {SDPA_ERR_SCRATCH_LIMIT}
 
 _lib = None
 
@@ -82,6 +83,9 @@ def library():
     L.sdpa_hip_bwd_dkdv.restype = i32
     L.sdpa_hip_bwd_dkdv.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, sz, i32, i32, i32, i32,
                                     i32, f32, f32, i32, u64, u64, vp]
+    L.sdpa_hip_bwd_noalloc.restype = i32
+    L.sdpa_hip_bwd_noalloc.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32,
+                                       i32, i32, f32, f32, i32, u64, u64, vp]
     L.sdpa_hip_drop_threshold.restype = u64
     L.sdpa_hip_drop_threshold.argtypes = [f32]
     L.sdpa_hip_dropout_mask.restype = i32

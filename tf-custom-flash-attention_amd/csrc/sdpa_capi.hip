@@ -4,6 +4,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "sdpa_hip.h"
 #include "sdpa_device.h"
 #include "sdpa_launch.h"
@@ -112,6 +114,8 @@ const char* sdpa_hip_status_string(int status) {
         case SDPA_ERR_DROPOUT_RANGE: return "dropout must be < 1";
         case SDPA_ERR_WORKSPACE: return "backward workspace is too small";
         case SDPA_ERR_HIP: return "HIP runtime error";
+        case SDPA_ERR_SCRATCH_LIMIT:
+            return "B * S_q exceeds the static scratch of sdpa_hip_bwd_noalloc (2097152 query rows)";
         default: return "unknown sdpa status";
     }
 }
@@ -259,6 +263,63 @@ int sdpa_hip_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, co
     return bwd_entry(sdpa::kBwdDkDv, dtype, q, k, v, nullptr, stats, d_o, nullptr, dk, dv,
                      const_cast<void*>(workspace), workspace_bytes, B, S_q, S_kv, D_qk, D_v, scale,
                      dropout, causal_mask, seed, offset, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Static scratch of sdpa_hip_bwd_noalloc: the backward's per-query-row
+// workspace (stats2, delta) for callers that cannot allocate.  Each device the
+// library runs on holds its own copy from module load until the process ends.
+// Host code never uses the array's name as an address (on the host it is a
+// stand-in, not device memory): the device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[SDPA_HIP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device id
+
+int scratch_on_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    if (dev < 0 || dev >= kMaxDevices) return hip_status(hipErrorInvalidDevice);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (ptr == nullptr) return hip_status(hipErrorInvalidSymbol);
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return SDPA_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int sdpa_hip_bwd_noalloc(int dtype, const void* q, const void* k, const void* v, const void* o,
+                         const float* stats, const void* d_o, void* dq, void* dk, void* dv, int B,
+                         int S_q, int S_kv, int D_qk, int D_v, float scale, float dropout,
+                         int causal_mask, uint64_t seed, uint64_t offset, hipStream_t stream) {
+    int st = check_common(dtype, B, S_q, S_kv, D_qk, D_v, dropout, causal_mask);
+    if (st != SDPA_OK) return st;
+    const size_t need = sdpa_hip_bwd_workspace_bytes(B, S_q);
+    if (need > (size_t)SDPA_HIP_NOALLOC_SCRATCH_BYTES) return SDPA_ERR_SCRATCH_LIMIT;
+    void* ws = nullptr;
+    if (need > 0) {
+        st = scratch_on_current_device(&ws);
+        if (st != SDPA_OK) return st;
+    }
+    // The kernels write every workspace row before reading it (dQ kernel,
+    // then dK/dV kernel on the same stream): nothing needs clearing.
+    return bwd_entry(sdpa::kBwdDq | sdpa::kBwdDkDv, dtype, q, k, v, o, stats, d_o, dq, dk, dv, ws,
+                     need, B, S_q, S_kv, D_qk, D_v, scale, dropout, causal_mask, seed, offset,
+                     stream);
 }
 
 uint64_t sdpa_hip_drop_threshold(float dropout) { return drop_threshold_impl(dropout); }
