@@ -558,13 +558,14 @@ void sdpa_bwd_dq_f32_kernel(const BwdParams p) {
         const float* Ks = lds + (blk & 1) * Cfg::STAGE;
         const float* Vs = Ks + Cfg::KT;
         const bool has_next = blk + 1 < nblk;
-        if (has_next) {
-            kst.load(Kb, kv0 + BN, S_kv - kv0 - BN, D_qk, D_qk, tid);
-            vst.load(Vb, kv0 + BN, S_kv - kv0 - BN, D_v, D_v, tid);
-        }
-
-        if (wave_live && (!causal || kv0 <= wave_last_q)) {
-            floatx16 sacc = floatx16{}, dpacc = floatx16{};
+        float* Kn = lds + ((blk + 1) & 1) * Cfg::STAGE;
+        // The next block is staged in two halves (V, then K) so that only one
+        // of them occupies registers at a time; the other buffer was released
+        // by every wave at the previous iteration's barrier.
+        if (has_next) vst.load(Vb, kv0 + BN, S_kv - kv0 - BN, D_v, D_v, tid);
+        const bool live = wave_live && (!causal || kv0 <= wave_last_q);
+        floatx16 sacc = floatx16{}, dpacc = floatx16{};
+        if (live) {
 #pragma unroll
             for (int u = 0; u < HQ / 4; ++u) {
                 const floatx4 kk = *reinterpret_cast<const floatx4*>(Ks + l32 * KS + HQ * hh + 4 * u);
@@ -577,6 +578,12 @@ void sdpa_bwd_dq_f32_kernel(const BwdParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) dpacc = mfma_f32(vv[e], dof[4 * u + e], dpacc);
             }
+        }
+        if (has_next) {
+            vst.template store<VS>(Kn + Cfg::KT, tid);
+            kst.load(Kb, kv0 + BN, S_kv - kv0 - BN, D_qk, D_qk, tid);
+        }
+        if (live) {
             const bool need_mask = (kv0 + BN > S_kv) || (causal && kv0 + BN - 1 > qw0);
             const uint64_t st_blk = DROP ? st_base + (uint64_t)kv0 * kLcgMul : 0;
             float ds[16];
@@ -605,11 +612,7 @@ void sdpa_bwd_dq_f32_kernel(const BwdParams p) {
                 }
         }
 
-        if (has_next) {
-            float* Kn = lds + ((blk + 1) & 1) * Cfg::STAGE;
-            kst.template store<KS>(Kn, tid);
-            vst.template store<VS>(Kn + Cfg::KT, tid);
-        }
+        if (has_next) kst.template store<KS>(Kn, tid);
         __syncthreads();
     }
 
@@ -703,8 +706,8 @@ void sdpa_bwd_dkdv_f32_kernel(const BwdParams p) {
     TileStage<float, BQ, DV, Cfg::NT, VEC> ost;
     float fpre = 0.f;
     auto load_rows = [&](int q0) {
-        qst.load(Qb, q0, S_q - q0, D_qk, D_qk, tid);
-        ost.load(dOb, q0, S_q - q0, D_v, D_v, tid);
+        qst.template load<false>(Qb, q0, S_q - q0, D_qk, D_qk, tid);
+        ost.template load<false>(dOb, q0, S_q - q0, D_v, D_v, tid);
         if (tid < 2 * BQ) {
             const int r = q0 + (tid & (BQ - 1));
             if (tid < BQ) fpre = r < S_q ? statsb[r] * kLog2e : INFINITY;

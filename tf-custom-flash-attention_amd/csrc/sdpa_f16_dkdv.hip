@@ -442,6 +442,9 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
             // Hash states after S: computed all at once above the MFMAs they
             // would hold 32 VGPRs through the chain.
             if constexpr (DROP) asm volatile("" : "+v"(st_sub) : "v"(sacc[15]));
+            // causal mask: query qs + 8 g + 4 hh + e is before key my_k iff
+            // my_k - qs - 4 hh > 8 g + e (one lane term, immediate bounds)
+            const int kd = MASK ? my_k - qs - 4 * hh : 0;
             uint32_t wx[8];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -449,7 +452,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float x = __builtin_fmaf(sacc[4 * g + e], sl2, -st4[g][e]);
-                    if (MASK && my_k > qs + 8 * g + 4 * hh + e) x = -INFINITY;
+                    if (MASK && kd > 8 * g + e) x = -INFINITY;
                     const float pr = fast_exp2(x);
                     const float pe = pr > kEps ? pr : 0.f;
                     if constexpr (DROP)
@@ -527,16 +530,9 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
                 }
             }
         };
-        // nsteps + 1 barriers, as many as the dS role.
-        for (int n = 0; n <= nsteps; ++n) {
-            __syncthreads();
-            if (n == nsteps) break;
+        auto general = [&](int n) {
             const int q0 = q_top - n * BQ;
             const uint32_t qbase = (uint32_t)((n % NSTAGE) * Cfg::STAGE);
-            if (sub_live(q0) && sub_live(q0 + 32) && !(CAUSAL && q0 < kw0 + 31)) {
-                full(qbase, n, q0);
-                continue;
-            }
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int qs = q0 + 32 * t;
@@ -544,7 +540,35 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
                 if (CAUSAL && qs < kw0 + 31) sub.template operator()<true>(qbase, n, t, qs);
                 else sub.template operator()<false>(qbase, n, t, qs);
             }
+        };
+        // The blocks that take `full` form one run [n0, n1): only the top
+        // block can lack its second sub-tile (q0 + 32 >= S_q) and, causal,
+        // the blocks past the first one that reaches the diagonal are
+        // masked.  The run has a loop of its own, so that the dV
+        // accumulators it carries stay in place (one loop over every kind of
+        // block merged them from the three paths with 64 register copies per
+        // block).  nsteps + 1 barriers, as many as the dS role.
+        int n0 = nsteps, n1 = nsteps;
+        if (kw0 < S_kv) {
+            n0 = (q_top + 32 < S_q) ? 0 : 1;
+            // full iff !(CAUSAL && q0 < kw0 + 31), q0 = q_top - 64 n
+            n1 = CAUSAL ? (q_top >= kw0 + 31 ? min(nsteps, (q_top - (kw0 + 31)) / BQ + 1) : 0) : nsteps;
+            n0 = min(n0, n1);
         }
+        int n = 0;
+        for (; n < n0; ++n) {
+            __syncthreads();
+            general(n);
+        }
+        for (; n < n1; ++n) {
+            __syncthreads();
+            full((uint32_t)((n % NSTAGE) * Cfg::STAGE), n, q_top - n * BQ);
+        }
+        for (; n < nsteps; ++n) {
+            __syncthreads();
+            general(n);
+        }
+        __syncthreads();
         if (key_ok) {
             half_t* dVb = static_cast<half_t*>(p.dv) + ((size_t)b * S_kv + my_k) * D_v;
             if (D_v == DV) store_rows_f16<DV>(dVb, dvacc, p.c.keep_scale, hh);

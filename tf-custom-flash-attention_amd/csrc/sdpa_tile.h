@@ -26,9 +26,31 @@ struct TileStage {
     uint4 r[PER_THREAD];
 
     // g: base of the [S, ld] matrix of this batch; rows row0.. are loaded,
-    // rows >= nrows and columns >= ncols read as zero.
+    // rows >= nrows and columns >= ncols read as zero.  With VEC the chunks
+    // are raw buffer loads over rows [row0, row0 + nrows): the descriptor's
+    // record count zero-fills rows past the end and a column past ncols gets
+    // an offset beyond every record, so the loads carry no branches (g and
+    // row0 are wave-uniform).
+    template <bool BUF = true>
     __device__ __forceinline__ void load(const T* __restrict__ g, int row0, int nrows, int ncols,
                                          int ld, int tid) {
+        if constexpr (VEC && BUF) {
+            const int row_bytes = ld * (int)sizeof(T);
+            const int max_rows = row_bytes > 0 ? 0x7FFFFFFF / row_bytes : 0x7FFFFFFF;
+            const int nrec = nrows <= 0 ? 0 : (nrows >= max_rows ? 0x7FFFFFFF : nrows * row_bytes);
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<T*>(g + (size_t)row0 * ld), (short)0, nrec, 0x00020000);
+#pragma unroll
+            for (int u = 0; u < PER_THREAD; ++u) {
+                const int c = tid + u * NTHREADS;
+                const int row = c / CPR;
+                const int col = (c % CPR) * EPC;
+                const bool ok = (NCH % NTHREADS == 0 || c < NCH) && col < ncols;
+                const uint32_t off = ok ? (uint32_t)(row * row_bytes + col * (int)sizeof(T)) : 0x80000000u;
+                r[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < PER_THREAD; ++u) {
             const int c = tid + u * NTHREADS;
