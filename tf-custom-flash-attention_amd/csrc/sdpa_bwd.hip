@@ -836,6 +836,267 @@ void sdpa_bwd_dkdv_f32_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// fp32 dK/dV with a 128-wide side: split roles.  One wave holding K, V, dK
+// and dV of 32 keys (plus S, dP and the staged tiles) needs more than 256
+// registers at D = 128, so each group of 32 keys gets two waves:
+//   P role  (waves 0-3): S = Q K^T, P~, dV^T += dO^T P~; P goes to LDS with
+//                        the dropout decision in its sign;
+//   dS role (waves 4-7): dP = dO V^T, dS from the partner's P, dK^T += Q^T dS,
+//                        one query block behind.
+// Eight waves share one workgroup barrier per block of 32 queries.  Blocks
+// pass through a ring of three LDS stages: in period n the P role reads
+// block n, the dS role block n - 1, and all 512 threads stage block n + 1
+// through registers into the third.  P of block m is exchanged through the
+// buffer m & 1 (written in period m, read in period m + 1).
+// ---------------------------------------------------------------------------
+#ifndef SDPA_F32_SPLIT
+#define SDPA_F32_SPLIT 1
+#endif
+template <int DQK, int DV>
+struct BwdKVF32SplitCfg {
+    static constexpr int NT = 512, BKV = 128, BQ = 32, NSTAGE = 3;
+    static constexpr int QS = DQK + 4, OS = DV + 4;
+    static constexpr int QT = BQ * QS, OT = BQ * OS;
+    static constexpr int STAGE = QT + OT + 2 * BQ;  // floats: Q, dO, stats2, delta
+    static constexpr int XB = 4 * 32 * 32;          // floats: P of 4 key groups x 32 queries
+    static constexpr size_t LDS_BYTES = (NSTAGE * (size_t)STAGE + 2 * (size_t)XB) * sizeof(float);
+    static_assert(LDS_BYTES <= 160 * 1024, "one workgroup per CU");
+};
+
+template <int DQK, int DV, bool VEC, bool DROP>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sdpa_bwd_dkdv_f32_split_kernel(const BwdParams p) {
+    using Cfg = BwdKVF32SplitCfg<DQK, DV>;
+    constexpr int BKV = Cfg::BKV, BQ = Cfg::BQ, QS = Cfg::QS, OS = Cfg::OS, NSTAGE = Cfg::NSTAGE;
+    constexpr int HQ = DQK / 2, HV = DV / 2;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    float* lds = reinterpret_cast<float*>(smem);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), kw = wave & 3;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
+    const bool causal = p.c.causal != 0;
+    const int tiles = (S_kv + BKV - 1) / BKV;
+    int b, kt;
+    map_tile(blockIdx.x, B, tiles, false, b, kt);
+    const int k0 = kt * BKV, kw0 = k0 + kw * 32, my_k = kw0 + l32;
+    const bool key_ok = my_k < S_kv;
+
+    const float* Qb = static_cast<const float*>(p.q) + (size_t)b * S_q * D_qk;
+    const float* dOb = static_cast<const float*>(p.d_o) + (size_t)b * S_q * D_v;
+    const float* statsb = p.stats + (size_t)b * S_q;
+    const float* deltab = p.delta + (size_t)b * S_q;
+
+    const int q_begin = causal ? (min(k0, S_q) / BQ) * BQ : 0;
+    const int nblk = (S_q - q_begin + BQ - 1) / BQ;
+    const bool wave_live = kw0 < S_kv;
+    // Block m is skipped by both roles when the key group sees none of it.
+    auto live = [&](int q0) { return wave_live && (!causal || q0 + BQ - 1 >= kw0); };
+    const float sl2 = p.c.scale_log2;
+    const float ksc = p.c.keep_scale;
+
+    TileStage<float, BQ, DQK, Cfg::NT, VEC> qst;
+    TileStage<float, BQ, DV, Cfg::NT, VEC> ost;
+    float fpre = 0.f;
+    auto load_rows = [&](int q0) {
+        qst.load(Qb, q0, S_q - q0, D_qk, D_qk, tid);
+        ost.load(dOb, q0, S_q - q0, D_v, D_v, tid);
+        if (tid < 2 * BQ) {
+            const int r = q0 + (tid & (BQ - 1));
+            if (tid < BQ) fpre = r < S_q ? statsb[r] * kLog2e : INFINITY;
+            else fpre = r < S_q ? deltab[r] : 0.f;
+        }
+    };
+    auto store_rows = [&](int s) {
+        float* base = lds + s * Cfg::STAGE;
+        qst.template store<QS>(base, tid);
+        ost.template store<OS>(base + Cfg::QT, tid);
+        if (tid < 2 * BQ) base[Cfg::QT + Cfg::OT + tid] = fpre;
+    };
+    // P of block m for this key group: 16 floats per lane, lane-contiguous.
+    auto xbuf = [&](int m) { return lds + NSTAGE * Cfg::STAGE + (m & 1) * Cfg::XB + kw * 1024; };
+
+    if (nblk > 0) {
+        load_rows(q_begin);
+        store_rows(0);
+    }
+
+    if (wave < 4) {
+        // ------------------------------------------------------------ P role
+        const float* Kb = static_cast<const float*>(p.k) + (size_t)b * S_kv * D_qk;
+        float kf[HQ];
+#pragma unroll
+        for (int u = 0; u < HQ / 4; ++u) {
+            const floatx4 f = __builtin_bit_cast(floatx4, load_row_chunk<float, VEC>(Kb, my_k, S_kv, HQ * hh + 4 * u, D_qk, D_qk));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kf[4 * u + e] = f[e];
+        }
+        const uint64_t st_base = DROP ? lcg_state(p.c.seed_offset, (uint64_t)b * S_q + 4 * hh, (uint64_t)S_kv, my_k) : 0;
+        const uint64_t row_step = (uint64_t)S_kv * kLcgMul;
+        const uint32_t thr = p.c.drop_threshold;
+        floatx16 dvacc[DV / 32];
+#pragma unroll
+        for (int dt = 0; dt < DV / 32; ++dt) dvacc[dt] = floatx16{};
+
+        for (int n = 0; n <= nblk; ++n) {
+            __syncthreads();
+            const bool has_next = n + 1 < nblk;
+            if (has_next) load_rows(q_begin + (n + 1) * BQ);
+            const int q0 = q_begin + n * BQ;
+            if (n < nblk && live(q0)) {
+                const float* Qs = lds + (n % NSTAGE) * Cfg::STAGE;
+                const float* dOs = Qs + Cfg::QT;
+                const float* Fs = dOs + Cfg::OT;
+                floatx16 sacc = floatx16{};
+#pragma unroll
+                for (int u = 0; u < HQ / 4; ++u) {
+                    const floatx4 qq = *reinterpret_cast<const floatx4*>(Qs + l32 * QS + HQ * hh + 4 * u);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) sacc = mfma_f32(qq[e], kf[4 * u + e], sacc);
+                }
+                const bool need_mask = !key_ok || (causal && q0 < kw0 + 31);
+                const uint64_t st_blk = DROP ? st_base + (uint64_t)q0 * row_step : 0;
+                float* xs = xbuf(n);
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int rb = 8 * g4 + 4 * hh;
+                    const floatx4 st4 = *reinterpret_cast<const floatx4*>(Fs + rb);
+                    floatx4 xv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * g4 + e;
+                        float x = __builtin_fmaf(sacc[r], sl2, -st4[e]);
+                        if (need_mask) {
+                            const int q = q0 + rb + e;
+                            if (!key_ok || (causal && my_k > q)) x = -INFINITY;
+                        }
+                        const float pr = fast_exp2(x);
+                        const float p0 = pr > kEps ? pr : 0.f;
+                        float pkk = p0;
+                        if constexpr (DROP) {
+                            const bool keep = lcg_keep(st_blk + (uint64_t)(8 * g4 + e) * row_step, thr);
+                            pkk = keep ? p0 : 0.f;
+                            xv[e] = keep ? p0 : -p0;
+                        } else {
+                            xv[e] = p0;
+                        }
+                        sacc[r] = pkk;
+                    }
+                    *reinterpret_cast<floatx4*>(xs + (g4 * 64 + lane) * 4) = xv;
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
+#pragma unroll
+                    for (int dt = 0; dt < DV / 32; ++dt)
+                        dvacc[dt] = mfma_f32(dOs[qrow * OS + 32 * dt + l32], sacc[r], dvacc[dt]);
+                }
+            }
+            if (has_next) store_rows((n + 1) % NSTAGE);
+        }
+        if (key_ok) {
+            float* dVb = static_cast<float*>(p.dv) + ((size_t)b * S_kv + my_k) * D_v;
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+                    floatx4 fv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) fv[e] = dvacc[dt][4 * g4 + e] * ksc;
+                    if constexpr (VEC) {
+                        if (d0 < D_v) *reinterpret_cast<floatx4*>(dVb + d0) = fv;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (d0 + e < D_v) dVb[d0 + e] = fv[e];
+                    }
+                }
+        }
+    } else {
+        // ----------------------------------------------------------- dS role
+        const float* Vb = static_cast<const float*>(p.v) + (size_t)b * S_kv * D_v;
+        float vf[HV];
+#pragma unroll
+        for (int u = 0; u < HV / 4; ++u) {
+            const floatx4 f = __builtin_bit_cast(floatx4, load_row_chunk<float, VEC>(Vb, my_k, S_kv, HV * hh + 4 * u, D_v, D_v));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vf[4 * u + e] = f[e];
+        }
+        floatx16 dkacc[DQK / 32];
+#pragma unroll
+        for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};
+
+        for (int n = 0; n <= nblk; ++n) {
+            __syncthreads();
+            const bool has_next = n + 1 < nblk;
+            if (has_next) load_rows(q_begin + (n + 1) * BQ);
+            const int m = n - 1;
+            const int q0 = q_begin + m * BQ;
+            if (m >= 0 && live(q0)) {
+                const float* Qs = lds + (m % NSTAGE) * Cfg::STAGE;
+                const float* dOs = Qs + Cfg::QT;
+                const float* Fs = dOs + Cfg::OT;
+                floatx16 dpacc = floatx16{};
+#pragma unroll
+                for (int u = 0; u < HV / 4; ++u) {
+                    const floatx4 oo = *reinterpret_cast<const floatx4*>(dOs + l32 * OS + HV * hh + 4 * u);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dpacc = mfma_f32(oo[e], vf[4 * u + e], dpacc);
+                }
+                // dS = P0 (keep ? dP / (1-p) : 0 - delta), P0 = |x|, keep = x > 0
+                const float* xs = xbuf(m);
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const floatx4 xv = *reinterpret_cast<const floatx4*>(xs + (g4 * 64 + lane) * 4);
+                    const floatx4 de4 = *reinterpret_cast<const floatx4*>(Fs + BQ + 8 * g4 + 4 * hh);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * g4 + e;
+                        float dpk = DROP ? dpacc[r] * ksc : dpacc[r];
+                        float p0 = xv[e];
+                        if constexpr (DROP) {
+                            dpk = xv[e] > 0.f ? dpk : 0.f;
+                            p0 = __builtin_fabsf(xv[e]);
+                        }
+                        dpacc[r] = p0 * (dpk - de4[e]);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int qrow = 8 * (r >> 2) + 4 * hh + (r & 3);
+#pragma unroll
+                    for (int dt = 0; dt < DQK / 32; ++dt)
+                        dkacc[dt] = mfma_f32(Qs[qrow * QS + 32 * dt + l32], dpacc[r], dkacc[dt]);
+                }
+            }
+            if (has_next) store_rows((n + 1) % NSTAGE);
+        }
+        if (key_ok) {
+            const float sc = p.c.scale;
+            float* dKb = static_cast<float*>(p.dk) + ((size_t)b * S_kv + my_k) * D_qk;
+#pragma unroll
+            for (int dt = 0; dt < DQK / 32; ++dt)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int d0 = 32 * dt + 8 * g4 + 4 * hh;
+                    floatx4 fv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) fv[e] = dkacc[dt][4 * g4 + e] * sc;
+                    if constexpr (VEC) {
+                        if (d0 < D_qk) *reinterpret_cast<floatx4*>(dKb + d0) = fv;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (d0 + e < D_qk) dKb[d0 + e] = fv[e];
+                    }
+                }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host launcher: dQ (+ delta) first, then dK/dV, on the caller's stream.
 // ---------------------------------------------------------------------------
 hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, int phases, hipStream_t stream) {
@@ -861,12 +1122,18 @@ hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, int phases, hip
                     } else {
                         using CQ = BwdQF32Cfg<DQK, DV>;
                         using CK = BwdKVF32Cfg<DQK, DV>;
+                        using CS = BwdKVF32SplitCfg<DQK, DV>;
                         const unsigned gq = (unsigned)(((S_q + CQ::BM - 1) / CQ::BM) * B);
                         const unsigned gk = (unsigned)(((S_kv + CK::BKV - 1) / CK::BKV) * B);
                         if (phases & kBwdDq)
                             err = launch_kernel<sdpa_bwd_dq_f32_kernel<DQK, DV, V, D>>(gq, CQ::NT, CQ::LDS_BYTES, stream, p);
-                        if (err == hipSuccess && (phases & kBwdDkDv))
-                            err = launch_kernel<sdpa_bwd_dkdv_f32_kernel<DQK, DV, V, D>>(gk, CK::NT, CK::LDS_BYTES, stream, p);
+                        if (err == hipSuccess && (phases & kBwdDkDv)) {
+                            if (SDPA_F32_SPLIT && (DQK == 128 || DV == 128))
+                                err = launch_kernel<sdpa_bwd_dkdv_f32_split_kernel<DQK, DV, V, D>>(
+                                    (unsigned)(((S_kv + CS::BKV - 1) / CS::BKV) * B), CS::NT, CS::LDS_BYTES, stream, p);
+                            else
+                                err = launch_kernel<sdpa_bwd_dkdv_f32_kernel<DQK, DV, V, D>>(gk, CK::NT, CK::LDS_BYTES, stream, p);
+                        }
                     }
                     return err;
                 });
