@@ -97,7 +97,7 @@ void sdpa_bwd_dq_f16_kernel(const BwdParams p) {
     const float stats2 = row_ok ? p.stats[row_q] * kLog2e : INFINITY;
     if (row_ok && hh == 0) {
         p.delta[row_q] = delta;
-        p.stats2[row_q] = stats2;
+        p.stats2[row_q] = stats2 + kGateShift;
     }
     const float sl2 = p.c.scale_log2;
     const float ksc = p.c.keep_scale;
@@ -527,7 +527,7 @@ void sdpa_bwd_dq_f32_kernel(const BwdParams p) {
     const float stats2 = row_ok ? p.stats[row_q] * kLog2e : INFINITY;
     if (row_ok && hh == 0) {
         p.delta[row_q] = delta;
-        p.stats2[row_q] = stats2;
+        p.stats2[row_q] = stats2 + kGateShift;
     }
     const float sl2 = p.c.scale_log2;
     const float ksc = p.c.keep_scale;

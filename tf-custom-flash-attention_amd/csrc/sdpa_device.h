@@ -38,6 +38,14 @@ constexpr uint64_t kLcgInc = 1442695040888963407ULL;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// The backward's P <= 1e-6 gate without a compare.  v_exp_f32 returns +0 for
+// every argument below -126 (its results never go denormal, whatever the
+// denormal mode), so P' = exp2(x - kGateShift) is 0 exactly when
+// P = exp2(x) < 2^(kGateShift - 126) = 1e-6, and P = P' * kGateScale
+// otherwise (kGateScale = 2^kGateShift).  The fp16 DMA backward kernels
+// evaluate P' and fold kGateScale into factors they apply anyway.
+constexpr float kGateShift = 106.068428f;   // 126 + log2(1e-6)
+constexpr float kGateScale = 8.50703884e31f;  // 2^kGateShift
 // Running-max sentinel in the log2 domain: finite, so exp2(x - m) never sees
 // (-inf) - (-inf); masked scores are -inf and contribute exactly 0.
 constexpr float kMaxSentinel = -1e30f;

@@ -151,8 +151,9 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     for (int dt = 0; dt < DV / 32; ++dt) dvacc[dt] = floatx16{};
 
     // Element-wise part of one 32-query sub-tile: the accumulator rows are
-    // queries qs + 8 g + 4 hh + e; st4 / de4 hold their stats * log2(e) and
-    // delta.  Produces the fp16 B operands P~ (for dV) and dS (for dK).
+    // queries qs + 8 g + 4 hh + e; st4 / de4 hold their stats2
+    // (stats log2(e) + kGateShift) and delta.  Produces the fp16 B operands
+    // P~ (for dV) and dS (for dK).
     auto elem = [&]<bool MASK>(const floatx16& sacc, const floatx16& dpacc, const floatx4 (&st4)[4],
                                const floatx4 (&de4)[4], int qs, half8& pk0, half8& pk1, half8& ds0, half8& ds1) {
         const uint64_t st_sub = DROP ? st_lane + (uint64_t)qs * row_step : 0;
@@ -163,10 +164,13 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int r = 4 * g + e;
+                // stats2 carries kGateShift: exp2 gives P' (0 where P <= 1e-6)
                 float x = __builtin_fmaf(sacc[r], sl2, -st4[g][e]);
-                if (MASK && my_k > qs + 8 * g + 4 * hh + e) x = -INFINITY;
-                float pr = fast_exp2(x);
-                pr = pr > kEps ? pr : 0.f;
+                // masked: keys after the query (causal) and rows past S_q, whose
+                // zero-filled stats2 would make P = 2^kGateShift
+                if (MASK && ((CAUSAL && my_k > qs + 8 * g + 4 * hh + e) || qs + 8 * g + 4 * hh + e >= S_q))
+                    x = -INFINITY;
+                const float pr = fast_exp2(x) * kGateScale;
                 if constexpr (DROP) {
                     const bool keep = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr);
                     pk4[e] = keep ? pr : 0.f;
@@ -313,18 +317,12 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     // (top-down walk); the causal diagonal and the blocks below it follow.
     // (Only the one-wave-per-SIMD shape has the registers for the pipeline;
     // the others run every step through the simple sub-tile path.)
+    // The top block is pipelined only when it lies entirely below S_q.
     const int n_full = Cfg::WAVES != 1 || kw0 >= S_kv ? 0
                        : !CAUSAL                      ? nsteps
                                    : (q_top >= kw0 + 32 ? min(nsteps, (q_top - kw0 - 32) / BQ + 1) : 0);
     int step = 0;
-    if constexpr (Cfg::WAVES == 1) {
-        for (; step < n_full; ++step) {
-            sync_step(step);
-            full_step((uint32_t)((step % NSTAGE) * Cfg::STAGE), q_top - step * BQ);
-            next_copy(step);
-        }
-    }
-    for (; step < nsteps; ++step) {
+    auto masked_step = [&](int step) {
         sync_step(step);
         if (kw0 < S_kv) {
             const int q0 = q_top - step * BQ;
@@ -333,11 +331,20 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
             for (int t = 0; t < 2; ++t) {
                 const int qs = q0 + 32 * t;
                 if (qs >= S_q || (CAUSAL && qs + 31 < kw0)) continue;
-                masked_sub(qbase, t, qs, CAUSAL && qs < kw0 + 31);
+                masked_sub(qbase, t, qs, (CAUSAL && qs < kw0 + 31) || qs + 32 > S_q);
             }
         }
         next_copy(step);
+    };
+    if constexpr (Cfg::WAVES == 1) {
+        if (n_full > 0 && q_top + BQ > S_q) masked_step(step++);
+        for (; step < n_full; ++step) {
+            sync_step(step);
+            full_step((uint32_t)((step % NSTAGE) * Cfg::STAGE), q_top - step * BQ);
+            next_copy(step);
+        }
     }
+    for (; step < nsteps; ++step) masked_step(step);
 
     if (key_ok) {
         half_t* dKb = static_cast<half_t*>(p.dk) + ((size_t)b * S_kv + my_k) * D_qk;
@@ -354,7 +361,8 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
 // ===========================================================================
 // Eight waves over 128 keys.  Waves w and w + 4 (w < 4) own keys
 // k0 + 32 w .. + 31 and run on the same SIMD:
-//   wave w      (P role):  S = Q K^T, P = exp2(S sl2 - stats2), P~ = P * keep,
+//   wave w      (P role):  S = Q K^T, P = exp2(S sl2 - stats2) 2^kGateShift
+//                          (stats2 carries the shift; see kGateShift), P~ = P * keep,
 //                          dV^T += dO^T P~; it hands P to wave w + 4 through
 //                          LDS with the dropout decision in the sign (-P for a
 //                          dropped element);
@@ -442,9 +450,12 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
             // Hash states after S: computed all at once above the MFMAs they
             // would hold 32 VGPRs through the chain.
             if constexpr (DROP) asm volatile("" : "+v"(st_sub) : "v"(sacc[15]));
-            // causal mask: query qs + 8 g + 4 hh + e is before key my_k iff
-            // my_k - qs - 4 hh > 8 g + e (one lane term, immediate bounds)
+            // masked: query qs + 8 g + 4 hh + e is before key my_k (causal) iff
+            // my_k - qs - 4 hh > 8 g + e, and past S_q iff 8 g + e >= S_q - qs - 4 hh
+            // (its zero-filled stats2 would make P = 2^kGateShift); one lane
+            // term each, against immediate bounds
             const int kd = MASK ? my_k - qs - 4 * hh : 0;
+            const int qd = MASK ? S_q - qs - 4 * hh : 0;
             uint32_t wx[8];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -452,9 +463,9 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float x = __builtin_fmaf(sacc[4 * g + e], sl2, -st4[g][e]);
-                    if (MASK && kd > 8 * g + e) x = -INFINITY;
-                    const float pr = fast_exp2(x);
-                    const float pe = pr > kEps ? pr : 0.f;
+                    if (MASK && ((CAUSAL && kd > 8 * g + e) || 8 * g + e >= qd)) x = -INFINITY;
+                    // stats2 carries kGateShift: exp2 gives P' (0 where P <= 1e-6)
+                    const float pe = fast_exp2(x) * kGateScale;
                     if constexpr (DROP)
                         x4[e] = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr) ? pe : -pe;
                     else
@@ -537,12 +548,12 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
             for (int t = 0; t < 2; ++t) {
                 const int qs = q0 + 32 * t;
                 if (!sub_live(qs)) continue;
-                if (CAUSAL && qs < kw0 + 31) sub.template operator()<true>(qbase, n, t, qs);
+                if ((CAUSAL && qs < kw0 + 31) || qs + 32 > S_q) sub.template operator()<true>(qbase, n, t, qs);
                 else sub.template operator()<false>(qbase, n, t, qs);
             }
         };
         // The blocks that take `full` form one run [n0, n1): only the top
-        // block can lack its second sub-tile (q0 + 32 >= S_q) and, causal,
+        // block can reach past S_q (it then takes the masked path) and, causal,
         // the blocks past the first one that reaches the diagonal are
         // masked.  The run has a loop of its own, so that the dV
         // accumulators it carries stay in place (one loop over every kind of
@@ -550,7 +561,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         // block).  nsteps + 1 barriers, as many as the dS role.
         int n0 = nsteps, n1 = nsteps;
         if (kw0 < S_kv) {
-            n0 = (q_top + 32 < S_q) ? 0 : 1;
+            n0 = (q_top + BQ <= S_q) ? 0 : 1;
             // full iff !(CAUSAL && q0 < kw0 + 31), q0 = q_top - 64 n
             n1 = CAUSAL ? (q_top >= kw0 + 31 ? min(nsteps, (q_top - (kw0 + 31)) / BQ + 1) : 0) : nsteps;
             n0 = min(n0, n1);

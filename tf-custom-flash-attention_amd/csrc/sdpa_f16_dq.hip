@@ -76,11 +76,15 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
     const float stats2 = row_ok ? p.stats[row_q] * kLog2e : INFINITY;
     if (row_ok && hh == 0) {
         p.delta[row_q] = delta;
-        p.stats2[row_q] = stats2;
+        p.stats2[row_q] = stats2 + kGateShift;
     }
     const float sl2 = p.c.scale_log2;
-    const float ksc = p.c.keep_scale;
-    const float nst = -stats2;
+    // P' = exp2(S sl2 - stats2 - kGateShift) is 0 where P <= 1e-6 and P / 2^kGateShift
+    // elsewhere: dS = P' (keep ? dP (1/(1-p)) - delta : -delta) 2^kGateShift, the
+    // factor taken into the two per-row constants.
+    const float nst = -(stats2 + kGateShift);
+    const float kscg = p.c.keep_scale * kGateScale;
+    const float deltag = delta * kGateScale;
 
     TileDma<BN, LK, 4> kd;
     TileDma<BN, LV, 4> vd;
@@ -126,17 +130,21 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
                     const int key = k0 + 8 * (rr >> 2) + 4 * hh + (rr & 3);
                     if (key >= S_kv || (CAUSAL && key > my_q)) x = -INFINITY;
                 }
-                const float pr = fast_exp2(x);
+                const float pg = fast_exp2(x);  // P', gated
                 float tt;
                 if constexpr (DROP) {
                     const bool keep = lcg_keep(st_blk + (uint64_t)(8 * (rr >> 2) + (rr & 3)) * kLcgMul, thr);
-                    tt = keep ? __builtin_fmaf(dpacc[rr], ksc, -delta) : -delta;
+                    tt = keep ? __builtin_fmaf(dpacc[rr], kscg, -deltag) : -deltag;
                 } else {
-                    tt = dpacc[rr] - delta;
+                    tt = __builtin_fmaf(dpacc[rr], kscg, -deltag);  // kscg = 2^kGateShift here
                 }
-                ds2[e] = pr > kEps ? pr * tt : 0.f;
+                ds2[e] = pg * tt;
             }
             w[r >> 1] = pack_h2(ds2[0], ds2[1]);
+            // without dropout the compiler otherwise runs the exponentials
+            // far ahead and spills at D = 128 (the copy offsets, whose
+            // reloads then wait for the copies in flight)
+            if constexpr (!DROP) __builtin_amdgcn_sched_barrier(0);
         }
         ds0 = half8_of(w[0], w[1], w[2], w[3]);
         ds1 = half8_of(w[4], w[5], w[6], w[7]);

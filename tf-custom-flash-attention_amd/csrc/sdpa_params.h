@@ -44,7 +44,7 @@ struct BwdParams {
     void* dk;
     void* dv;
     // Workspace, written by the dQ kernel and read by the dK/dV kernel:
-    float* stats2;  // [B, S_q]: stats_i * log2(e)
+    float* stats2;  // [B, S_q]: stats_i * log2(e) + kGateShift (sdpa_device.h)
     float* delta;   // [B, S_q]: delta_i = sum_d dO[i,d] * O[i,d]
     AttnShape s;
     AttnScalars c;
