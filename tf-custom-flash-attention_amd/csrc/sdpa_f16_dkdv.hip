@@ -42,6 +42,11 @@ namespace {
 #ifndef SDPA_DKDV_SPLIT
 #define SDPA_DKDV_SPLIT 1
 #endif
+// Split-role kernel, who copies the tiles: 0 the dS role; 1 the P role under
+// the causal mask, else the dS role; 2 the P role.
+#ifndef SDPA_DKDV_PCOPY
+#define SDPA_DKDV_PCOPY 1
+#endif
 
 
 template <int DQK, int DV>
@@ -370,7 +375,10 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
 //                          dK^T += Q^T dS, one block behind the P role.
 // Each role holds one operand (K or V, 32 VGPRs) and one accumulator (64), so
 // both roles fit two waves per SIMD, and every SIMD still does the four GEMMs
-// of its 32 keys once per block.  The dS role also copies the tiles.
+// of its 32 keys once per block.  The tiles are copied by the P role under
+// the causal mask (it issues them right after its S chains, in time it would
+// otherwise spend waiting at the barrier for the dS role) and by the dS role
+// otherwise (there the P role has no registers to spare for the copy state).
 //
 // LDS: a ring of three blocks (Q, dO, stats2, delta) and two P exchange
 // buffers.  During step n the P role reads block n, the dS role reads block
@@ -393,6 +401,7 @@ template <int DQK, int DV, bool CAUSAL, bool DROP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
     using Cfg = DkvSplitCfg<DQK, DV>;
+    constexpr bool PCOPY = SDPA_DKDV_PCOPY == 2 || (SDPA_DKDV_PCOPY == 1 && CAUSAL);
     constexpr int BKV = Cfg::BKV, BQ = Cfg::BQ, LQ = Cfg::LQ, LO = Cfg::LO, NSTAGE = Cfg::NSTAGE;
 
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
@@ -438,6 +447,41 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         SwzLane<LO> swO;
         swQ.init(lane);
         swO.init(lane);
+        // Tile copies (PCOPY).  Block m + 1 goes out while this role works on block m,
+        // right after its S chains: its stage held block m - 2, which the dS
+        // role released at barrier m, and it lands before barrier m + 1.  The
+        // dS role, which issued them before, has no time to spare: this
+        // role waited at the barrier for it (the dS role's tail, or the copies
+        // split between the roles, measured slower).  With dropout the delta
+        // row of each block is then rewritten as delta' (see the dS role) by
+        // the wave that copied it.
+        const float* st2b = p.stats2 + (size_t)b * S_q;
+        const float* deltab = p.delta + (size_t)b * S_q;
+        TileDma<BQ, LQ, 4> qd;
+        TileDma<BQ, LO, 4> od;
+        qd.init(kw, lane, D_qk * 2, D_qk / 8);
+        od.init(kw, lane, D_v * 2, D_v / 8);
+        auto issue_block = [&](int m) {
+            if (PCOPY && m < nsteps) {
+                const int q0 = q_top - m * BQ;
+                unsigned char* st = smem + (m % NSTAGE) * Cfg::STAGE;
+                qd.issue(make_rsrc(Qb + (size_t)q0 * D_qk, (long long)(S_q - q0) * D_qk * 2), st, kw);
+                od.issue(make_rsrc(dOb + (size_t)q0 * D_v, (long long)(S_q - q0) * D_v * 2), st + Cfg::QB, kw);
+                if (kw == 0) dma4(make_rsrc(st2b + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB, lane * 4);
+                if (kw == 1) dma4(make_rsrc(deltab + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB + BQ * 4, lane * 4);
+            }
+        };
+        auto land_block = [&](int m) {
+            if (PCOPY && m < nsteps) {
+                wait_vm();
+                if (DROP && kw == 1) {
+                    float* dl = reinterpret_cast<float*>(smem + (m % NSTAGE) * Cfg::STAGE + Cfg::QB + Cfg::OB) + BQ;
+                    dl[lane] = dl[lane] / p.c.keep_scale;
+                }
+            }
+        };
+        issue_block(0);
+        land_block(0);
         floatx16 dvacc[DV / 32];
 #pragma unroll
         for (int dt = 0; dt < DV / 32; ++dt) dvacc[dt] = floatx16{};
@@ -513,7 +557,11 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         // wave and its dS partner, released by the same barrier, started
         // every block with an MFMA burst and then both ran VALU work
         // (3% slower).
-        auto full = [&](uint32_t qbase, int m, int q0) {
+        // after_s runs once both S chains are issued (the tile copies: the
+        // wave's issue stall behind the CU's copy queue then overlaps the
+        // chains; spread over the block, the copies stalled its element-wise
+        // work instead, 4% slower).
+        auto full = [&](uint32_t qbase, int m, int q0, auto&& after_s) {
             const uint32_t obase = qbase + Cfg::QB;
             const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
             const uint32_t aQ = qbase + swQ.row;
@@ -524,6 +572,9 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
                 for (int ks = 0; ks < DQK / 16; ++ks)
                     sacc[t] = mfma_f16(lds_row<LQ>(aQ, ks, 32 * t), kreg[ks], sacc[t]);
+            __builtin_amdgcn_sched_barrier(0);
+            after_s();
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 floatx4 st4[4];
@@ -570,14 +621,19 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         for (; n < n0; ++n) {
             __syncthreads();
             general(n);
+            issue_block(n + 1);
+            land_block(n + 1);
         }
         for (; n < n1; ++n) {
             __syncthreads();
-            full((uint32_t)((n % NSTAGE) * Cfg::STAGE), n, q_top - n * BQ);
+            full((uint32_t)((n % NSTAGE) * Cfg::STAGE), n, q_top - n * BQ, [&] { issue_block(n + 1); });
+            land_block(n + 1);
         }
         for (; n < nsteps; ++n) {
             __syncthreads();
             general(n);
+            issue_block(n + 1);
+            land_block(n + 1);
         }
         __syncthreads();
         if (key_ok) {
@@ -613,8 +669,8 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
             if (kw == 0) dma4(make_rsrc(st2b + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB, lane * 4);
             if (kw == 1) dma4(make_rsrc(deltab + q0, (long long)(S_q - q0) * 4), st + Cfg::QB + Cfg::OB + BQ * 4, lane * 4);
         };
-        if (nsteps > 0) issue(0);
-        if (nsteps > 1) issue(1);
+        if (!PCOPY && nsteps > 0) issue(0);
+        if (!PCOPY && nsteps > 1) issue(1);
         SwzLane<LQ> swQ;
         SwzLane<LO> swO;
         swQ.init(lane);
@@ -669,6 +725,21 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
                 dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t + 16), ds1, dkacc[dt]);
             }
         };
+        if constexpr (PCOPY) {
+        // The P role copies every block and rewrites its delta row before the
+        // barrier that releases it: this role only multiplies.  nsteps + 1
+        // barriers, as many as the P role: barrier n releases block n - 1 to
+        // this role.
+        __syncthreads();
+        for (int n = 1; n <= nsteps; ++n) {
+            __syncthreads();
+            const int m = n - 1;
+            const int q0 = q_top - m * BQ;
+            const uint32_t qbase = (uint32_t)((m % NSTAGE) * Cfg::STAGE);
+            if (sub_live(q0)) sub(qbase, m, 0);
+            if (sub_live(q0 + 32)) sub(qbase, m, 1);
+        }
+        } else {
         for (int n = 0; n <= nsteps; ++n) {
             // block n has landed (block 1 may still fly at n = 0)
             if (n == 0 && nsteps > 1) wait_vm_n<LPS>();
@@ -698,6 +769,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
             if (sub_live(q0)) sub(qbase, m, 0);
             if (cp) od.issue(make_rsrc(dOb + (size_t)qn * D_v, (long long)(S_q - qn) * D_v * 2), stn + Cfg::QB, kw);
             if (sub_live(q0 + 32)) sub(qbase, m, 1);
+        }
         }
         if (key_ok) {
             half_t* dKb = static_cast<half_t*>(p.dk) + ((size_t)b * S_kv + my_k) * D_qk;
