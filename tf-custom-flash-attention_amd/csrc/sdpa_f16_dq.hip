@@ -155,7 +155,7 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
     // and waits out the whole LDS latency every time); the transposed reads
     // for dQ go out before the element-wise work and land during it.
     constexpr int NK = DQK / 16, NV = DV / 16, RD_FULL = SDPA_RD;
-    auto sub = [&]<bool PART>(uint32_t kbase, int k0, int t) {
+    auto sub = [&]<bool PART>(uint32_t kbase, int k0, int t, auto&& after_chains) {
         // masked sub-tiles read one operand ahead: their mask code needs the
         // registers (RD ahead spills at D = 128)
         constexpr int RD = PART ? 1 : RD_FULL;
@@ -174,6 +174,8 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
             else dpacc = mfma_f16(op[i], doreg[i - NK], dpacc);
             __builtin_amdgcn_sched_barrier(0);
         }
+        after_chains();
+        __builtin_amdgcn_sched_barrier(0);
         half8 at[2][DQK / 32];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
@@ -193,16 +195,25 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
         __syncthreads();
         if (step + 1 < nsteps) issue(step + 1);
     };
+    auto none = [] {};
     // Steps whose 64 keys are all visible to all 32 queries of the wave come
     // first (no mask code); the causal diagonal and the key tail follow.
     const int full_lim = CAUSAL ? min(qw0 - (BN - 1), S_kv - BN) : S_kv - BN;
     const int n_full = qw0 >= S_q ? 0 : min(nsteps, full_lim < 0 ? 0 : full_lim / BN + 1);
+    // In these steps the copies of step + 1 go out once the first sub-tile's
+    // S/dP chains are issued, so that the wave's issue stall overlaps them
+    // (issued right after the barrier, the copy burst of the four waves held
+    // each of them ~560 clk per step).  An L2 prefetch of the step after next
+    // (one dword per line) made the kernel slower.
     int step = 0;
     for (; step < n_full; ++step) {
-        sync_step(step);
+        wait_vm();
+        __syncthreads();
         const uint32_t kbase = (uint32_t)((step & 1) * Cfg::STAGE);
-        sub.template operator()<false>(kbase, step * BN, 0);
-        sub.template operator()<false>(kbase, step * BN + 32, 1);
+        sub.template operator()<false>(kbase, step * BN, 0, [&] {
+            if (step + 1 < nsteps) issue(step + 1);
+        });
+        sub.template operator()<false>(kbase, step * BN + 32, 1, none);
     }
     for (; step < nsteps; ++step) {
         sync_step(step);
@@ -213,8 +224,8 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
         for (int t = 0; t < 2; ++t) {
             const int k0 = kv0 + 32 * t;
             if (!(k0 < S_kv && (!CAUSAL || k0 <= qw0 + 31))) continue;
-            if (k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0)) sub.template operator()<true>(kbase, k0, t);
-            else sub.template operator()<false>(kbase, k0, t);
+            if (k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0)) sub.template operator()<true>(kbase, k0, t, none);
+            else sub.template operator()<false>(kbase, k0, t, none);
         }
     }
 
