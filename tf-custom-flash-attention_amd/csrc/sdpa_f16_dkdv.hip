@@ -290,7 +290,7 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
 
     // One 32-query sub-tile that needs the causal mask (or lies past it),
     // computed without pipelining: qs = first query, t = 0 / 1 within the step.
-    auto masked_sub = [&](uint32_t qbase, int t, int qs, bool part) {
+    auto masked_sub = [&](uint32_t qbase, int t, int qs, bool part) __attribute__((always_inline)) {
         const uint32_t obase = qbase + Cfg::QB;
         const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
         const uint32_t aQ = qbase + swQ.row, aO = obase + swO.row;
@@ -320,11 +320,13 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
 
     // Steps whose 64 queries all see all 32 keys of the wave come first
     // (top-down walk); the causal diagonal and the blocks below it follow.
-    // (Only the one-wave-per-SIMD shape has the registers for the pipeline;
-    // the others run every step through the simple sub-tile path.)
-    // The top block is pipelined only when it lies entirely below S_q.
-    const int n_full = Cfg::WAVES != 1 || kw0 >= S_kv ? 0
-                       : !CAUSAL                      ? nsteps
+    // Only the one-wave-per-SIMD shape has the registers for the pipelined
+    // step; the others run the full steps as two plain sub-tiles, in a loop
+    // of their own: one loop over every kind of step merged the dK/dV
+    // accumulators of its paths with 32 register copies per sub-tile.
+    // The top block takes the full path only when it lies entirely below S_q.
+    const int n_full = kw0 >= S_kv ? 0
+                       : !CAUSAL   ? nsteps
                                    : (q_top >= kw0 + 32 ? min(nsteps, (q_top - kw0 - 32) / BQ + 1) : 0);
     int step = 0;
     auto masked_step = [&](int step) {
@@ -341,8 +343,17 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
         }
         next_copy(step);
     };
-    if constexpr (Cfg::WAVES == 1) {
-        if (n_full > 0 && q_top + BQ > S_q) masked_step(step++);
+    if (n_full > 0 && q_top + BQ > S_q) masked_step(step++);
+    if constexpr (Cfg::WAVES != 1) {
+        for (; step < n_full; ++step) {
+            sync_step(step);
+            const int q0 = q_top - step * BQ;
+            const uint32_t qbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE);
+            masked_sub(qbase, 0, q0, false);
+            masked_sub(qbase, 1, q0 + 32, false);
+            next_copy(step);
+        }
+    } else {
         for (; step < n_full; ++step) {
             sync_step(step);
             full_step((uint32_t)((step % NSTAGE) * Cfg::STAGE), q_top - step * BQ);
