@@ -322,3 +322,72 @@ def test_empty_inputs(pkg):
             assert torch.all(s == np.float32(-1e9) + np.float32(np.log(np.float32(1e-6))))
         if S_q == 0 and B * S_kv:
             assert torch.all(dk == 0) and torch.all(dv == 0)
+
+
+def _bwd_f64_gated(q, k, v, o, stats, d_o, scale, thresh):
+    """float64 gradients of non-causal attention without dropout from the
+    forward's statistics, skipping every element with P <= thresh (the
+    reference's backward, sdpa/sdpa_bwd.cu.cc:130-170), for the threshold
+    sensitivity check below."""
+    q, k, v, o, d_o = (a.astype(np.float64) for a in (q, k, v, o, d_o))
+    P = np.exp(scale * np.einsum("bid,bjd->bij", q, k) - stats.astype(np.float64)[..., None])
+    P = np.where(P > thresh, P, 0.0)
+    delta = (d_o * o).sum(-1, keepdims=True)
+    dS = P * (np.einsum("bid,bjd->bij", d_o, v) - delta)
+    return (scale * np.einsum("bij,bjd->bid", dS, k), scale * np.einsum("bij,bid->bjd", dS, q),
+            np.einsum("bij,bid->bjd", P, d_o))
+
+
+@pytest.mark.parametrize("dt", ["f16", "f32"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("p", [0.0, 0.1])
+def test_gate_threshold_elements(pkg, O, dt, D, p):
+    """Many probabilities on both sides of the backward's 1e-6 gate, each
+    carrying a large dP, so that gating them or not moves the gradients far
+    beyond the tolerance.  Key 0 dominates every row (score 0, value row 0);
+    key j >= 1 has score q_i0 ln(t_j) with t_j log-uniform in [3e-7, 3e-6]
+    and q_i0 in {0.95, 1, 1.05}, so P_ij ~ t_j^q_i0 spans the threshold; V is
+    scaled so that dP ~ 4e3 and dS ~ 4e-3 per gated-or-not element.  The
+    kernels (exp2's flush in the fp16 DMA kernels, a compare elsewhere) are
+    checked against the oracle at the north_star tolerances; without dropout
+    the case is also shown to separate the threshold: float64 references with
+    the gate at 5e-7 and 2e-6 lie well outside the tolerance of the kernel's
+    result, the one at 1e-6 inside it.  fp32 gets the summation allowance of
+    the other shapes outside the BASELINE configs (1e-5 + 2 sqrt(L) 2^-24
+    max|g|, L = S_kv)."""
+    B, S_q, S_kv = 2, 64, 2048
+    rng = np.random.Generator(np.random.PCG64(2024 + D))
+    q = np.zeros((B, S_q, D), np.float32)
+    q[:, :, 0] = np.array([0.95, 1.0, 1.05, 1.0])[np.arange(S_q) % 4]
+    k = rng.standard_normal((B, S_kv, D), dtype=np.float32)
+    k[:, 0, :] = 0.0
+    k[:, 1:, 0] = np.log(np.exp(rng.uniform(np.log(3e-7), np.log(3e-6), (B, S_kv - 1))))
+    v = (rng.standard_normal((B, S_kv, D), dtype=np.float32) * 1000.0)
+    v[:, 0, :] = 0.0
+    d_o = rng.standard_normal((B, S_q, D), dtype=np.float32) * 0.25
+    ndt = np_dtype(dt)
+    q, k, v, d_o = (a.astype(ndt) for a in (q, k, v, d_o))
+    seed, off = 5, 77
+    print(f"[case] gate {dt} D={D} p={p}", flush=True)
+    o, s = pkg.sdpa(_t(q), _t(k), _t(v), seed, off, dropout=p, scale=1.0)
+    dq, dk, dv = pkg.sdpa_grad(_t(q), _t(k), _t(v), o, s, _t(d_o), seed, off, dropout=p, scale=1.0)
+    torch.cuda.synchronize()
+    o, s, g = _np(o), _np(s), [_np(t) for t in (dq, dk, dv)]
+    f32 = lambda a: a.astype(np.float32)
+    kw = dict(scale=1.0, dropout=p, seed=seed, offset=off)
+    refs = O.sdpa_bwd_gate(f32(q), f32(k), f32(v), f32(o), s, f32(d_o), **kw)
+    gmax = max(float(np.abs(r).max()) for r in refs)
+    tol = TOL[dt]["grad"] + (2 * np.sqrt(S_kv) * 2.0 ** -24 * gmax if dt == "f32" else 0.0)
+    errs = [maxabs(a, r) for a, r in zip(g, refs)]
+    print(f"[errs] gate {dt} D={D} p={p}: dq/dk/dv vs oracle " + "/".join(f"{e:.2e}" for e in errs)
+          + f" (tol {tol:.2e})", flush=True)
+    assert max(errs) <= tol
+    if p == 0.0:
+        at = lambda th: _bwd_f64_gated(q, k, v, o, s, d_o, 1.0, th)
+        ref1, lo, hi = at(1e-6), at(5e-7), at(2e-6)
+        # dK carries the gated elements most directly (dK_j = sum_i dS_ij q_i)
+        sep_lo, sep_hi = maxabs(lo[1], ref1[1]), maxabs(hi[1], ref1[1])
+        print(f"[sep] dK moves {sep_lo:.2e} (gate 5e-7) and {sep_hi:.2e} (gate 2e-6)", flush=True)
+        assert min(sep_lo, sep_hi) > 4 * TOL["f16"]["grad"]
+        assert maxabs(g[1], ref1[1]) <= tol
+        assert min(maxabs(g[1], lo[1]), maxabs(g[1], hi[1])) > 3 * TOL["f16"]["grad"]
