@@ -591,6 +591,15 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
                 floatx4 st4[4];
 #pragma unroll
                 for (int g = 0; g < 4; ++g) st4[g] = *reinterpret_cast<const floatx4*>(Fs + 32 * t + 8 * g + 4 * hh);
+                // The dV operands go out before the element-wise work and land
+                // during it (read just before each MFMA, every MFMA waited
+                // out the LDS latency: 2.5% slower).
+                half8 at[2][DV / 32];
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int dt = 0; dt < DV / 32; ++dt) at[j][dt] = lds_tr<LO>(aO0, aO1, dt, 32 * t + 16 * j);
+                __builtin_amdgcn_sched_barrier(0);
                 half8 pk0, pk1, xv0, xv1;
                 elem.template operator()<false>(sacc[t], st4, q0 + 32 * t, pk0, pk1, xv0, xv1);
                 unsigned char* xs = xbuf(m, t);
@@ -598,8 +607,8 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
                 *reinterpret_cast<half8*>(xs + 1024) = xv1;
 #pragma unroll
                 for (int dt = 0; dt < DV / 32; ++dt) {
-                    dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t), pk0, dvacc[dt]);
-                    dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t + 16), pk1, dvacc[dt]);
+                    dvacc[dt] = mfma_f16(at[0][dt], pk0, dvacc[dt]);
+                    dvacc[dt] = mfma_f16(at[1][dt], pk1, dvacc[dt]);
                 }
             }
         };
@@ -728,12 +737,20 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) de4[g] = *reinterpret_cast<const floatx4*>(Fs + BQ + 32 * t + 8 * g + 4 * hh);
             const unsigned char* xs = xbuf(m, t);
+            const half8 xv0 = *reinterpret_cast<const half8*>(xs), xv1 = *reinterpret_cast<const half8*>(xs + 1024);
+            // the dK operands land during the element-wise work, as in the P role
+            half8 at[2][DQK / 32];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int dt = 0; dt < DQK / 32; ++dt) at[j][dt] = lds_tr<LQ>(aQ0, aQ1, dt, 32 * t + 16 * j);
+            __builtin_amdgcn_sched_barrier(0);
             half8 ds0, ds1;
-            elem(dpacc, de4, *reinterpret_cast<const half8*>(xs), *reinterpret_cast<const half8*>(xs + 1024), ds0, ds1);
+            elem(dpacc, de4, xv0, xv1, ds0, ds1);
 #pragma unroll
             for (int dt = 0; dt < DQK / 32; ++dt) {
-                dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t), ds0, dkacc[dt]);
-                dkacc[dt] = mfma_f16(lds_tr<LQ>(aQ0, aQ1, dt, 32 * t + 16), ds1, dkacc[dt]);
+                dkacc[dt] = mfma_f16(at[0][dt], ds0, dkacc[dt]);
+                dkacc[dt] = mfma_f16(at[1][dt], ds1, dkacc[dt]);
             }
         };
         if constexpr (PCOPY) {
