@@ -290,7 +290,7 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
 
     // One 32-query sub-tile that needs the causal mask (or lies past it),
     // computed without pipelining: qs = first query, t = 0 / 1 within the step.
-    auto masked_sub = [&](uint32_t qbase, int t, int qs, bool part) __attribute__((always_inline)) {
+    auto masked_sub = [&]<bool PART>(uint32_t qbase, int t, int qs) __attribute__((always_inline)) {
         const uint32_t obase = qbase + Cfg::QB;
         const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
         const uint32_t aQ = qbase + swQ.row, aO = obase + swO.row;
@@ -304,8 +304,7 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
         floatx4 fs[4], fd[4];
         read_f(Fs, t, fs, fd);
         half8 pk0, pk1, ds0, ds1;
-        if (part) elem.template operator()<true>(sacc, dpacc, fs, fd, qs, pk0, pk1, ds0, ds1);
-        else elem.template operator()<false>(sacc, dpacc, fs, fd, qs, pk0, pk1, ds0, ds1);
+        elem.template operator()<PART>(sacc, dpacc, fs, fd, qs, pk0, pk1, ds0, ds1);
 #pragma unroll
         for (int dt = 0; dt < DV / 32; ++dt) {
             dvacc[dt] = mfma_f16(lds_tr<LO>(aO0, aO1, dt, 32 * t), pk0, dvacc[dt]);
@@ -338,7 +337,10 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
             for (int t = 0; t < 2; ++t) {
                 const int qs = q0 + 32 * t;
                 if (qs >= S_q || (CAUSAL && qs + 31 < kw0)) continue;
-                masked_sub(qbase, t, qs, (CAUSAL && qs < kw0 + 31) || qs + 32 > S_q);
+                // every live sub-tile takes the masked path: with the
+                // unmasked one as well, the loop merged the dK/dV
+                // accumulators of the two with 64 register copies per step
+                masked_sub.template operator()<true>(qbase, t, qs);
             }
         }
         next_copy(step);
@@ -349,8 +351,8 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
             sync_step(step);
             const int q0 = q_top - step * BQ;
             const uint32_t qbase = (uint32_t)((step % NSTAGE) * Cfg::STAGE);
-            masked_sub(qbase, 0, q0, false);
-            masked_sub(qbase, 1, q0 + 32, false);
+            masked_sub.template operator()<false>(qbase, 0, q0);
+            masked_sub.template operator()<false>(qbase, 1, q0 + 32);
             next_copy(step);
         }
     } else {
@@ -618,9 +620,8 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int qs = q0 + 32 * t;
-                if (!sub_live(qs)) continue;
-                if ((CAUSAL && qs < kw0 + 31) || qs + 32 > S_q) sub.template operator()<true>(qbase, n, t, qs);
-                else sub.template operator()<false>(qbase, n, t, qs);
+                // the masked path for every live sub-tile (see the dV note below)
+                if (sub_live(qs)) sub.template operator()<true>(qbase, n, t, qs);
             }
         };
         // The blocks that take `full` form one run [n0, n1): only the top
@@ -629,7 +630,8 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         // masked.  The run has a loop of its own, so that the dV
         // accumulators it carries stay in place (one loop over every kind of
         // block merged them from the three paths with 64 register copies per
-        // block).  nsteps + 1 barriers, as many as the dS role.
+        // block; the loops around it run the masked path only, for the same
+        // reason).  nsteps + 1 barriers, as many as the dS role.
         int n0 = nsteps, n1 = nsteps;
         if (kw0 < S_kv) {
             n0 = (q_top + BQ <= S_q) ? 0 : 1;

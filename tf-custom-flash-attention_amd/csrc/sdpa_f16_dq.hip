@@ -197,7 +197,10 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
     };
     auto none = [] {};
     // Steps whose 64 keys are all visible to all 32 queries of the wave come
-    // first (no mask code); the causal diagonal and the key tail follow.
+    // first (no mask code); the causal diagonal and the key tail follow, every
+    // live sub-tile through the masked path (with the unmasked path as well,
+    // the loop merged the dQ accumulators of the two with 130 register
+    // copies per step).
     const int full_lim = CAUSAL ? min(qw0 - (BN - 1), S_kv - BN) : S_kv - BN;
     const int n_full = qw0 >= S_q ? 0 : min(nsteps, full_lim < 0 ? 0 : full_lim / BN + 1);
     // In these steps the copies of step + 1 go out once the first sub-tile's
@@ -224,8 +227,7 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
         for (int t = 0; t < 2; ++t) {
             const int k0 = kv0 + 32 * t;
             if (!(k0 < S_kv && (!CAUSAL || k0 <= qw0 + 31))) continue;
-            if (k0 + 32 > S_kv || (CAUSAL && k0 + 31 > qw0)) sub.template operator()<true>(kbase, k0, t, none);
-            else sub.template operator()<false>(kbase, k0, t, none);
+            sub.template operator()<true>(kbase, k0, t, none);
         }
     }
 
