@@ -62,5 +62,8 @@ hipError_t launch_fwd_f16_dma(const FwdParams& p, hipStream_t stream);
 hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream);
 // dQ phase of launch_bwd_f16_dma (sdpa_f16_dq.hip)
 hipError_t launch_bwd_dq_f16_dma(const BwdParams& p, hipStream_t stream);
+// dK/dV phase of launch_bwd_f16_dma at a 128-wide side (D_qk or D_v = 128;
+// sdpa_f16_dkdv_split.hip)
+hipError_t launch_bwd_dkdv_f16_split(const BwdParams& p, hipStream_t stream);
 
 }  // namespace sdpa
