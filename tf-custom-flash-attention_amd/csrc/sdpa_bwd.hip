@@ -53,10 +53,16 @@ struct BwdQF16Cfg {
     static constexpr int NT = 256, BM = 128, BN = 64;
     static constexpr int KT = BN * DQK, VT = BN * DV, STAGE = KT + VT;
     static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE * sizeof(half_t);
+    // waves per SIMD: at D_qk = 128 (with D_v >= 64) the kernel needs more
+    // than 256 registers (two waves per SIMD spilled 44-148 bytes per lane in
+    // the loop), so it runs one wave per SIMD with the whole register file:
+    // 8-11% faster at D = 124 and 124 / 60
+    static constexpr int WAVES = (DQK == 128 && DV >= 64) ? 1 : 2;
 };
 
 template <int DQK, int DV, bool VEC, bool DROP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(BwdQF16Cfg<DQK, DV>::WAVES, BwdQF16Cfg<DQK, DV>::WAVES)))
 void sdpa_bwd_dq_f16_kernel(const BwdParams p) {
     using Cfg = BwdQF16Cfg<DQK, DV>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = DQK / 8, LV = DV / 8;
@@ -238,10 +244,16 @@ struct BwdKVF16Cfg {
     static constexpr int QT = BQ * DQK, OT = BQ * DV;            // halves
     static constexpr int STAGE_BYTES = (QT + OT) * 2 + 2 * BQ * 4;  // + stats2[BQ], delta[BQ]
     static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE_BYTES;
+    // one wave per SIMD at D_qk = D_v = 128, where K, V, dK and dV of a
+    // 32-key group do not fit 256 registers (two waves spilled 148-184 bytes
+    // per lane in the loop; one wave is 23% faster at D = 124).  At 128 / 64
+    // two waves spill 20-44 bytes and are still 2.5% faster than one.
+    static constexpr int WAVES = (DQK == 128 && DV == 128) ? 1 : 2;
 };
 
 template <int DQK, int DV, bool VEC, bool DROP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(BwdKVF16Cfg<DQK, DV>::WAVES, BwdKVF16Cfg<DQK, DV>::WAVES)))
 void sdpa_bwd_dkdv_f16_kernel(const BwdParams p) {
     using Cfg = BwdKVF16Cfg<DQK, DV>;
     constexpr int BKV = Cfg::BKV, BQ = Cfg::BQ, LQ = DQK / 8, LO = DV / 8;
@@ -477,10 +489,19 @@ struct BwdQF32Cfg {
     static constexpr int KS = DQK + 4, VS = DV + 4;
     static constexpr int KT = BN * KS, VT = BN * VS, STAGE = KT + VT;
     static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE * sizeof(float);
+    // one wave per SIMD where two spilled in the loop: D_qk = D_v = 128
+    // (184-228 bytes per lane; one wave 19% faster), and D_qk = 128 / D_v =
+    // 64 with the generic row loads (40-56 bytes; 3% faster).  Aligned 128 /
+    // 64 with dropout keeps two waves: 20 bytes of spill, 4.6% faster than
+    // one; c5's shape (aligned, no dropout) fits two waves.
+    template <bool VEC, bool DROP>
+    static constexpr int waves() { return (DQK == 128 && (DV == 128 || (DV == 64 && !VEC))) ? 1 : 2; }
 };
 
 template <int DQK, int DV, bool VEC, bool DROP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(BwdQF32Cfg<DQK, DV>::template waves<VEC, DROP>(),
+                                   BwdQF32Cfg<DQK, DV>::template waves<VEC, DROP>())))
 void sdpa_bwd_dq_f32_kernel(const BwdParams p) {
     using Cfg = BwdQF32Cfg<DQK, DV>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, KS = Cfg::KS, VS = Cfg::VS;
@@ -1128,7 +1149,7 @@ hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, int phases, hip
                         if (phases & kBwdDq)
                             err = launch_kernel<sdpa_bwd_dq_f32_kernel<DQK, DV, V, D>>(gq, CQ::NT, CQ::LDS_BYTES, stream, p);
                         if (err == hipSuccess && (phases & kBwdDkDv)) {
-                            if (SDPA_F32_SPLIT && (DQK == 128 || DV == 128))
+                            if constexpr (SDPA_F32_SPLIT && (DQK == 128 || DV == 128))
                                 err = launch_kernel<sdpa_bwd_dkdv_f32_split_kernel<DQK, DV, V, D>>(
                                     (unsigned)(((S_kv + CS::BKV - 1) / CS::BKV) * B), CS::NT, CS::LDS_BYTES, stream, p);
                             else
