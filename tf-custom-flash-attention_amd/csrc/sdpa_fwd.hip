@@ -56,6 +56,10 @@ struct FwdF16Cfg {
     static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE * sizeof(half_t);
 };
 
+// Two waves per SIMD throughout: with the split-variant loop beside the main
+// one, <128,128> (aligned rows, no dropout) keeps 20 bytes per lane in
+// scratch and <64,128> (generic row loads, no dropout) 8; one wave per SIMD,
+// spill-free, measured 5-6.5% slower at D = 124 and 60 / 124.
 template <int DQK, int DV, bool VEC, bool DROP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_fwd_f16_kernel(const FwdParams p) {
@@ -117,7 +121,11 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
     }
     __syncthreads();
 
-    for (int blk = 0; blk < nblk; ++blk) {
+    // One key block.  SPLIT (rows that see at most BN keys in all): P~
+    // enters the PV product as two fp16 parts, hi + lo.  Over one or two keys
+    // the fp16 rounding of P~ (2^-12 relative) would move o by more than half
+    // an fp16 ulp; over many keys it averages out.
+    auto block = [&]<bool SPLIT>(int blk) {
         const int kv0 = blk * BN;
         const half_t* Ks = lds + (blk & 1) * Cfg::STAGE;
         const half_t* Vs = Ks + Cfg::KT;
@@ -170,7 +178,7 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
             // ---- probabilities, dropout, fp16 B operands ------------------
             const uint64_t st_blk = DROP ? st_base + (uint64_t)kv0 * kLcgMul : 0;
             float lsum = 0.f;
-            half8 pb[BN / 16];
+            half8 pb[BN / 16], pl[BN / 16];
 #pragma unroll
             for (int t = 0; t < BN / 32; ++t) {
 #pragma unroll
@@ -189,6 +197,11 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
                     const int s = 2 * t + (r >> 3), i = r & 7;
                     pb[s][i] = hp[0];
                     pb[s][i + 1] = hp[1];
+                    if constexpr (SPLIT) {
+                        const half2v hl = cvt_pk(p0 - (float)hp[0], p1 - (float)hp[1]);
+                        pl[s][i] = hl[0];
+                        pl[s][i + 1] = hl[1];
+                    }
                 }
             }
             l_run += lsum;
@@ -201,6 +214,7 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
                     const half4 a1 = lds_read_tr(Vs + swz_off<LV>(16 * s + 8 + tr_row, 32 * dt + tr_col));
                     const half8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
                     oacc[dt] = mfma_f16(a, pb[s], oacc[dt]);
+                    if constexpr (SPLIT) oacc[dt] = mfma_f16(a, pl[s], oacc[dt]);
                 }
             }
         }
@@ -211,6 +225,15 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
             vst.store_swz(Kn + Cfg::KT, tid);
         }
         __syncthreads();
+    };
+    // Only waves whose rows all lie below key BN (or S_kv < BN) take the
+    // split, and for them the first block is the only visible one: such a
+    // wave runs the split variant in a loop of its own (one loop choosing per
+    // block merged the accumulators of the two variants with register copies).
+    if (S_kv < BN || (causal && qw0 < BN - 1)) {
+        for (int blk = 0; blk < nblk; ++blk) block.template operator()<true>(blk);
+    } else {
+        for (int blk = 0; blk < nblk; ++blk) block.template operator()<false>(blk);
     }
 
     // ---- epilogue: stats and O = acc / l ----------------------------------
