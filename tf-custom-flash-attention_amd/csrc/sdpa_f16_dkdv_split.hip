@@ -222,11 +222,12 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         // wave and its dS partner, released by the same barrier, started
         // every block with an MFMA burst and then both ran VALU work
         // (3% slower).
-        // after_s runs once both S chains are issued (the tile copies: the
-        // wave's issue stall behind the CU's copy queue then overlaps the
-        // chains; spread over the block, the copies stalled its element-wise
-        // work instead, 4% slower).
-        auto full = [&](uint32_t qbase, int m, int q0, auto&& after_s) {
+        // after_s runs once both S chains are issued, after_e0 once the
+        // first sub-tile's P is written (the tile copies: a wave's issue
+        // stall behind the CU's copy queue then overlaps work already in
+        // flight; one wave's copies spread over the block stalled its
+        // element-wise work instead, 4% slower).
+        auto full = [&](uint32_t qbase, int m, int q0, auto&& after_s, auto&& after_e0) {
             const uint32_t obase = qbase + Cfg::QB;
             const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
             const uint32_t aQ = qbase + swQ.row;
@@ -259,6 +260,11 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
                 unsigned char* xs = xbuf(m, t);
                 *reinterpret_cast<half8*>(xs) = xv0;
                 *reinterpret_cast<half8*>(xs + 1024) = xv1;
+                if (t == 0) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    after_e0();
+                    __builtin_amdgcn_sched_barrier(0);
+                }
 #pragma unroll
                 for (int dt = 0; dt < DV / 32; ++dt) {
                     dvacc[dt] = mfma_f16(at[0][dt], pk0, dvacc[dt]);
@@ -300,7 +306,14 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
         }
         for (; n < n1; ++n) {
             __syncthreads();
-            full((uint32_t)((n % NSTAGE) * Cfg::STAGE), n, q_top - n * BQ, [&] { issue_block(n + 1); });
+            // Waves 0-1 issue their copies after the S chains, waves 2-3
+            // after the first sub-tile's P: issued by all four at once, each
+            // wave's copies queued behind the others' in the CU's address
+            // unit (≈720 clk of issue stall per block; staggered, c4 dK/dV
+            // 0.5-1.5% faster; a third point after dV(0) gained nothing).
+            full((uint32_t)((n % NSTAGE) * Cfg::STAGE), n, q_top - n * BQ,
+                 [&] { if (kw < 2) issue_block(n + 1); },
+                 [&] { if (kw >= 2) issue_block(n + 1); });
             land_block(n + 1);
         }
         for (; n < nsteps; ++n) {
