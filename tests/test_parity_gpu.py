@@ -139,6 +139,10 @@ EDGE = [
     ("f16", 2, 1000, 1000, 32, 32, True, 0.2),
     ("f16", 3, 200, 700, 64, 64, False, 0.1),
     ("f16", 2, 513, 513, 128, 64, True, 0.0),
+    # B a multiple of 8: the DMA kernels interleave the tiles of 2 (B = 16)
+    # and 3 (B = 24) batch rows per XCD
+    ("f16", 16, 640, 640, 64, 64, True, 0.1),
+    ("f16", 24, 300, 300, 128, 128, True, 0.0),
     ("f32", 2, 1, 1, 8, 8, False, 0.0),
     ("f32", 1, 2048, 2048, 128, 128, True, 0.1),
     ("f32", 3, 77, 77, 64, 64, True, 0.0),

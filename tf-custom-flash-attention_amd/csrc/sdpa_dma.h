@@ -186,18 +186,37 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 // Workgroup id -> (batch, tile), XCD-major: ids are dealt round-robin over
 // the 8 XCDs (id % 8); XCD x owns a contiguous range of the batch-major tile
 // list, so the K/V (or Q/dO) rows a tile streams are shared in that XCD's L2
-// by the other tiles of its batch row.  `reverse` runs the tiles of a batch
-// row last-first (causal query tiles: the heaviest first).
-// (An order that runs the heaviest tiles of all of an XCD's rows first made
-// each kernel faster on its own but the next kernel of the fwd/bwd sequence
-// slower by more, at the c4 shape: the row order is kept.)
-__device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles, bool reverse, int& b, int& t) {
+// by the other tiles of its batch row.  Inside that range the tiles of `win`
+// consecutive batch rows are interleaved (tile-major within the window), and
+// `reverse` runs a row's tiles last-first (causal query tiles: the heaviest
+// first).  Interleaving starts the heavy tiles of all rows of a window
+// together, so the light ones fill the end of the launch; row by row, the
+// last rows' heavy tiles started late and ran alone.  win = 1 is plain row
+// order; row_window() picks it.
+__device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles, bool reverse, int win, int& b, int& t) {
     const int xcd = bid & 7, local = bid >> 3;
     const int per = nblocks >> 3, rem = nblocks & 7;
     const int lin = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-    b = lin / tiles;
-    const int r = lin - b * tiles;
+    const int g = lin / (win * tiles);
+    const int k = lin - g * (win * tiles);
+    const int nr = min(win, nblocks / tiles - g * win);
+    const int r = k / nr;
+    b = g * win + (k - r * nr);
     t = reverse ? tiles - 1 - r : r;
+}
+
+// The xcd_map window for B batch rows that each stream row_bytes: the largest
+// divisor of the rows one XCD owns (B / 8) whose rows stream at most 8 MiB,
+// so windows never straddle two XCDs and their working set stays bounded; 1
+// (row order) when B is not a multiple of 8.  At B = 128 (16 rows per XCD)
+// and 2 MiB per row the c4 shape gets 4; at 0.5 MiB per row, 16.
+inline int row_window(int B, size_t row_bytes) {
+    if (B <= 0 || B % 8) return 1;
+    const int rows = B / 8;
+    int w = 1;
+    for (int d = 2; d <= rows; ++d)
+        if (rows % d == 0 && (size_t)d * row_bytes <= ((size_t)8 << 20)) w = d;
+    return w;
 }
 
 // Two fp32 values -> one dword of two RNE-rounded halves (v_cvt_pk_f16_f32).

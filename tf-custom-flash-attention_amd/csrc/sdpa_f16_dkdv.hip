@@ -60,7 +60,7 @@ struct DkvDmaCfg {
 
 template <int DQK, int DV, bool CAUSAL, bool DROP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DkvDmaCfg<DQK, DV>::WAVES, DkvDmaCfg<DQK, DV>::WAVES)))
-void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
+void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p, const int win) {
     using Cfg = DkvDmaCfg<DQK, DV>;
     constexpr int BKV = Cfg::BKV, BQ = Cfg::BQ, LQ = Cfg::LQ, LO = Cfg::LO;
 
@@ -69,7 +69,7 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p) {
     const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
     const int tiles = (S_kv + BKV - 1) / BKV;
     int b, kt;
-    xcd_map(blockIdx.x, B * tiles, tiles, false, b, kt);
+    xcd_map(blockIdx.x, B * tiles, tiles, false, win, b, kt);
     const int k0 = kt * BKV, kw0 = k0 + 32 * wave, my_k = kw0 + l32;
     const bool key_ok = my_k < S_kv;
 
@@ -392,7 +392,8 @@ hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream
                         } else {
                             const long long n = (long long)((S_kv + CK::BKV - 1) / CK::BKV) * B;
                             err = launch_kernel<sdpa_bwd_dkdv_f16_dma_kernel<DQK, DV, CA, DR>>(
-                                (unsigned)n, CK::NT, CK::LDS_BYTES, stream, p);
+                                (unsigned)n, CK::NT, CK::LDS_BYTES, stream, p,
+                                row_window(B, (size_t)S_q * (DQK + DV) * 2));
                         }
                     }
                     return err;

@@ -64,7 +64,7 @@ struct DkvSplitCfg {
 
 template <int DQK, int DV, bool CAUSAL, bool DROP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
+void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
     using Cfg = DkvSplitCfg<DQK, DV>;
     constexpr bool PCOPY = SDPA_DKDV_PCOPY == 2 || (SDPA_DKDV_PCOPY == 1 && CAUSAL);
     constexpr int BKV = Cfg::BKV, BQ = Cfg::BQ, LQ = Cfg::LQ, LO = Cfg::LO, NSTAGE = Cfg::NSTAGE;
@@ -75,7 +75,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p) {
     const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
     const int tiles = (S_kv + BKV - 1) / BKV;
     int b, kt;
-    xcd_map(blockIdx.x, B * tiles, tiles, false, b, kt);
+    xcd_map(blockIdx.x, B * tiles, tiles, false, win, b, kt);
     const int k0 = kt * BKV, kw0 = k0 + 32 * kw, my_k = kw0 + l32;
     const bool key_ok = my_k < S_kv;
 
@@ -490,7 +490,8 @@ hipError_t launch_bwd_dkdv_f16_split(const BwdParams& p, hipStream_t stream) {
                         using CS = DkvSplitCfg<DQK, DV>;
                         const long long n = (long long)((S_kv + CS::BKV - 1) / CS::BKV) * B;
                         return launch_kernel<sdpa_bwd_dkdv_f16_split_kernel<DQK, DV, CA, DR>>(
-                            (unsigned)n, CS::NT, CS::LDS_BYTES, stream, p);
+                            (unsigned)n, CS::NT, CS::LDS_BYTES, stream, p,
+                            row_window(B, (size_t)p.s.S_q * (DQK + DV) * 2));
                     } else {
                         return hipErrorInvalidValue;  // the one-wave kernel serves D <= 64
                     }

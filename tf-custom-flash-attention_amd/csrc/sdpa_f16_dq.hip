@@ -40,7 +40,7 @@ struct DqDmaCfg {
 template <int DQK, int DV, bool CAUSAL, bool DROP>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(DqDmaCfg<DQK, DV>::template wpe<DROP>(), DqDmaCfg<DQK, DV>::template wpe<DROP>())))
-void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
+void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p, const int win) {
     using Cfg = DqDmaCfg<DQK, DV>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV;
 
@@ -49,7 +49,7 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p) {
     const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
     const int tiles = (S_q + BM - 1) / BM;
     int b, qt;
-    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, b, qt);
+    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, win, b, qt);
     const int q0 = qt * BM, qw0 = q0 + 32 * wave, my_q = qw0 + l32;
     const size_t row_q = (size_t)b * S_q + my_q;
 
@@ -258,7 +258,8 @@ hipError_t launch_bwd_dq_f16_dma(const BwdParams& p, hipStream_t stream) {
                     using CQ = DqDmaCfg<DQK, DV>;
                     const long long n = (long long)((S_q + CQ::BM - 1) / CQ::BM) * B;
                     return launch_kernel<sdpa_bwd_dq_f16_dma_kernel<DQK, DV, CA, DR>>((unsigned)n, CQ::NT,
-                                                                                CQ::LDS_BYTES, stream, p);
+                                                                                CQ::LDS_BYTES, stream, p,
+                                                                                row_window(B, (size_t)p.s.S_kv * (DQK + DV) * 2));
                 });
             });
         });

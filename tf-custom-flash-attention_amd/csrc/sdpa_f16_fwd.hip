@@ -66,7 +66,7 @@ struct FwdDmaCfg {
 template <int DQK, int DV, bool CAUSAL, bool DROP>
 __global__ __launch_bounds__((FwdDmaCfg<DQK, DV>::NT))
 __attribute__((amdgpu_waves_per_eu(FwdDmaCfg<DQK, DV>::template wpe<DROP>(), FwdDmaCfg<DQK, DV>::template wpe<DROP>())))
-void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
+void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
     using Cfg = FwdDmaCfg<DQK, DV>;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, LV = Cfg::LV, NW = Cfg::NW, NSTAGE = Cfg::NSTAGE;
     constexpr int NKS = DQK / 16, NDT = DV / 32;
@@ -76,7 +76,7 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p) {
     const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk, D_v = p.s.D_v;
     const int tiles = (S_q + BM - 1) / BM;
     int b, qt;
-    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, b, qt);
+    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, win, b, qt);
     const int q0 = qt * BM, qw0 = q0 + 32 * wave, my_q = qw0 + l32;
 
     const half_t* Qb = static_cast<const half_t*>(p.q) + (size_t)b * S_q * D_qk;
@@ -377,7 +377,8 @@ hipError_t launch_fwd_f16_dma(const FwdParams& p, hipStream_t stream) {
                     using Cfg = FwdDmaCfg<DQK, DV>;
                     const long long n = (long long)((S_q + Cfg::BM - 1) / Cfg::BM) * B;
                     return launch_kernel<sdpa_fwd_f16_dma_kernel<DQK, DV, decltype(c)::value, decltype(d)::value>>(
-                        (unsigned)n, Cfg::NT, Cfg::LDS_BYTES, stream, p);
+                        (unsigned)n, Cfg::NT, Cfg::LDS_BYTES, stream, p,
+                        row_window(B, (size_t)p.s.S_kv * (DQK + DV) * 2));
                 });
             });
         });
