@@ -73,16 +73,18 @@ void sdpa_bwd_dq_f16_dma_kernel(const BwdParams p, const int win) {
     }
     const float delta = xhalf_sum(dpart);
     const bool row_ok = my_q < S_q;
-    const float stats2 = row_ok ? p.stats[row_q] * kLog2e : INFINITY;
+    // stats * log2(e) + kGateShift with one rounding (an explicit fma: left
+    // to contraction, the rounding depended on the code around it)
+    const float stats2g = row_ok ? __builtin_fmaf(p.stats[row_q], kLog2e, kGateShift) : INFINITY;
     if (row_ok && hh == 0) {
         p.delta[row_q] = delta;
-        p.stats2[row_q] = stats2 + kGateShift;
+        p.stats2[row_q] = stats2g;
     }
     const float sl2 = p.c.scale_log2;
     // P' = exp2(S sl2 - stats2 - kGateShift) is 0 where P <= 1e-6 and P / 2^kGateShift
     // elsewhere: dS = P' (keep ? dP (1/(1-p)) - delta : -delta) 2^kGateShift, the
     // factor taken into the two per-row constants.
-    const float nst = -(stats2 + kGateShift);
+    const float nst = -stats2g;
     const float kscg = p.c.keep_scale * kGateScale;
     const float deltag = delta * kGateScale;
 
