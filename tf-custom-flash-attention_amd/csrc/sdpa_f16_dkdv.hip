@@ -15,8 +15,9 @@
 // stages.
 //
 // Work order.  Workgroup ids are remapped so that each XCD (ids are dealt
-// round-robin over the 8 XCDs) walks whole batch rows: all tiles of a batch
-// row run on one XCD and share its L2 copy of the streamed operands.
+// round-robin over the 8 XCDs) owns whole batch rows: all tiles of a batch
+// row run on one XCD and share its L2 copy of the streamed operands; the
+// tiles of a window of rows are interleaved (xcd_map, row_window).
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16, fp32 accumulation; the lane
 // layouts are listed in sdpa_device.h), per group of 32 keys (lane = key):
