@@ -193,13 +193,15 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 // together, so the light ones fill the end of the launch; row by row, the
 // last rows' heavy tiles started late and ran alone.  win = 1 is plain row
 // order; row_window() picks it.
-__device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles, bool reverse, int win, int& b, int& t) {
+__host__ __device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles, bool reverse, int win, int& b,
+                                                  int& t) {
     const int xcd = bid & 7, local = bid >> 3;
     const int per = nblocks >> 3, rem = nblocks & 7;
     const int lin = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
     const int g = lin / (win * tiles);
     const int k = lin - g * (win * tiles);
-    const int nr = min(win, nblocks / tiles - g * win);
+    const int left = nblocks / tiles - g * win;  // rows from this window on
+    const int nr = win < left ? win : left;
     const int r = k / nr;
     b = g * win + (k - r * nr);
     t = reverse ? tiles - 1 - r : r;
