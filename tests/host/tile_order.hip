@@ -2,16 +2,19 @@
 // (xcd_map and row_window in sdpa_dma.h), built and run by
 // tests/test_tile_order.py.  No GPU call: xcd_map runs on the host.
 //
-// For every (B, tiles, row bytes, reverse) of a grid:
-//   - row_window is 1 when B is not a multiple of 8, else the largest divisor
-//     of B / 8 whose rows stream at most 8 MiB (1 if none);
+// With lin(b, t) = b * tiles + rank, rank = tiles-1-t when reversed (else t),
+// for every (B, tiles, row bytes, reverse) of a grid:
+//   - row_window(row bytes) = max(1, 8 MiB / row bytes);
 //   - workgroup ids 0 .. B*tiles-1 map one to one onto (batch, tile);
-//   - ids are dealt to XCDs as id % 8; with B a multiple of 8, XCD x gets
-//     exactly the batch rows [x B/8, (x+1) B/8);
-//   - in each XCD's dispatch order (id / 8 increasing), the windows of rows
-//     come one after another, and inside a window the tiles run by rank
-//     (rank = tiles-1-t when reversed, else t) with every row of the window
-//     taking rank r before any row takes rank r+1.
+//   - ids are dealt to XCDs as id % 8, and XCD x covers exactly the x-th of
+//     8 contiguous lin ranges, whose lengths (nblocks / 8, the first
+//     nblocks % 8 of them one longer) follow XCD order;
+//   - in its dispatch order (id / 8 increasing) an XCD runs ceil(n / (wcap
+//     tiles)) chunks of equal length (+-1, longer ones first) for its n ids;
+//     each chunk covers a contiguous lin range, the chunks advance through
+//     the XCD's range, and inside a chunk (rank, row) strictly increases;
+//   - with B a multiple of 8 and wcap dividing B / 8 (the c3 and c4 cases),
+//     every chunk is exactly wcap whole rows.
 #include <cstdio>
 #include <set>
 #include <vector>
@@ -32,54 +35,68 @@ static int fails = 0;
 
 int main() {
     const size_t kCap = (size_t)8 << 20;
-    const int Bs[] = {1, 2, 3, 7, 8, 9, 16, 24, 40, 64, 128, 136, 256};
-    const int Ts[] = {1, 2, 3, 5, 16, 32};
+    const int Bs[] = {1, 2, 3, 7, 8, 9, 12, 16, 20, 24, 36, 40, 56, 64, 100, 128, 136, 256};
+    const int Ts[] = {1, 2, 3, 4, 5, 6, 7, 8, 16, 32, 40};
+    const int Ws[] = {1, 2, 3, 4, 5, 7, 16, 42, 1 << 20};  // chunk caps (row_window values)
     const size_t RB[] = {1024, (size_t)128 << 10, (size_t)512 << 10, (size_t)2 << 20, (size_t)3 << 20,
                          (size_t)9 << 20};
     int cases = 0;
+    for (size_t rb : RB) {
+        const int w = sdpa::row_window(rb);
+        CHECK(w == (int)(kCap / rb > 0 ? kCap / rb : 1), "rb=%zu wcap=%d", rb, w);
+    }
     for (int B : Bs)
-        for (size_t rb : RB) {
-            const int win = sdpa::row_window(B, rb);
-            if (B % 8) {
-                CHECK(win == 1, "B=%d rb=%zu win=%d", B, rb, win);
-            } else {
-                const int rows = B / 8;
-                CHECK(win >= 1 && rows % win == 0, "B=%d rb=%zu win=%d", B, rb, win);
-                CHECK(win == 1 || (size_t)win * rb <= kCap, "B=%d rb=%zu win=%d", B, rb, win);
-                for (int d = win + 1; d <= rows; ++d)
-                    CHECK(rows % d != 0 || (size_t)d * rb > kCap, "B=%d rb=%zu win=%d d=%d", B, rb, win, d);
-            }
+        for (int wcap : Ws) {
             for (int T : Ts)
                 for (int rev = 0; rev < 2; ++rev) {
                     ++cases;
                     const int n = B * T;
                     std::vector<int> seen((size_t)n, 0);
-                    std::vector<std::vector<int>> bx(8), rx(8);  // per XCD, in dispatch order
+                    std::vector<std::vector<int>> lx(8);  // per XCD: lin values in dispatch order
                     for (int bid = 0; bid < n; ++bid) {
                         int b = -1, t = -1;
-                        sdpa::xcd_map(bid, n, T, rev != 0, win, b, t);
+                        sdpa::xcd_map(bid, n, T, rev != 0, wcap, b, t);
                         CHECK(b >= 0 && b < B && t >= 0 && t < T, "B=%d T=%d bid=%d -> (%d,%d)", B, T, bid, b, t);
                         if (b < 0 || b >= B || t < 0 || t >= T) continue;
                         ++seen[(size_t)b * T + t];
-                        bx[bid & 7].push_back(b);
-                        rx[bid & 7].push_back(rev ? T - 1 - t : t);
+                        lx[bid & 7].push_back(b * T + (rev ? T - 1 - t : t));
                     }
                     for (int i = 0; i < n; ++i) CHECK(seen[i] == 1, "B=%d T=%d tile %d seen %d", B, T, i, seen[i]);
+                    int s_x = 0;
                     for (int x = 0; x < 8; ++x) {
-                        if (B % 8 == 0) {
-                            const std::set<int> rows(bx[x].begin(), bx[x].end());
-                            const int lo = x * (B / 8), hi = (x + 1) * (B / 8);
-                            CHECK((int)rows.size() == B / 8 && *rows.begin() == lo && *rows.rbegin() == hi - 1,
-                                  "B=%d T=%d xcd %d rows %zu", B, T, x, rows.size());
+                        const int n_x = n / 8 + (x < n % 8 ? 1 : 0);
+                        CHECK((int)lx[x].size() == n_x, "B=%d T=%d xcd %d has %zu ids", B, T, x, lx[x].size());
+                        if ((int)lx[x].size() != n_x) continue;
+                        const std::set<int> lins(lx[x].begin(), lx[x].end());
+                        CHECK(n_x == 0 || (*lins.begin() == s_x && *lins.rbegin() == s_x + n_x - 1 &&
+                                           (int)lins.size() == n_x),
+                              "B=%d T=%d xcd %d range", B, T, x);
+                        if (n_x > 0) {
+                            const int nch = (n_x + wcap * T - 1) / (wcap * T);
+                            const int base = n_x / nch, extra = n_x % nch;
+                            int pos = 0, prev_hi = s_x - 1;
+                            for (int j = 0; j < nch; ++j) {
+                                const int len = base + (j < extra ? 1 : 0);
+                                int lo = lx[x][pos], hi = lx[x][pos];
+                                for (int i = pos; i < pos + len; ++i) {
+                                    lo = lx[x][i] < lo ? lx[x][i] : lo;
+                                    hi = lx[x][i] > hi ? lx[x][i] : hi;
+                                    if (i > pos) {
+                                        const int r_a = lx[x][i - 1] % T, r_b = lx[x][i] % T;
+                                        const int w_a = lx[x][i - 1] / T, w_b = lx[x][i] / T;
+                                        CHECK(r_b > r_a || (r_b == r_a && w_b > w_a),
+                                              "B=%d T=%d wcap=%d xcd %d chunk %d pos %d not rank-major", B, T, wcap, x, j, i);
+                                    }
+                                }
+                                CHECK(hi - lo + 1 == len && lo == prev_hi + 1,
+                                      "B=%d T=%d wcap=%d xcd %d chunk %d [%d,%d] len %d", B, T, wcap, x, j, lo, hi, len);
+                                if (B % 8 == 0 && (B / 8) % wcap == 0)
+                                    CHECK(len == wcap * T && lo % T == 0, "B=%d T=%d wcap=%d chunk not whole rows", B, T, wcap);
+                                prev_hi = hi;
+                                pos += len;
+                            }
                         }
-                        // windows in order; inside one, rank-major over its rows
-                        for (size_t i = 1; i < bx[x].size(); ++i) {
-                            const int g0 = bx[x][i - 1] / win, g1 = bx[x][i] / win;
-                            CHECK(g1 >= g0, "B=%d T=%d xcd %d window order", B, T, x);
-                            if (g1 == g0)
-                                CHECK(rx[x][i] > rx[x][i - 1] || (rx[x][i] == rx[x][i - 1] && bx[x][i] > bx[x][i - 1]),
-                                      "B=%d T=%d win=%d xcd %d pos %zu", B, T, win, x, i);
-                        }
+                        s_x += n_x;
                     }
                 }
         }

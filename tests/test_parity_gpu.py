@@ -143,6 +143,10 @@ EDGE = [
     # and 3 (B = 24) batch rows per XCD
     ("f16", 16, 640, 640, 64, 64, True, 0.1),
     ("f16", 24, 300, 300, 128, 128, True, 0.0),
+    # B not a multiple of 8: each XCD's tile range starts and ends inside a
+    # batch row (1.5 and 4.5 rows per XCD), run rank-major as one chunk
+    ("f16", 12, 1024, 1024, 64, 64, True, 0.0),
+    ("f16", 36, 384, 384, 128, 128, True, 0.1),
     ("f32", 2, 1, 1, 8, 8, False, 0.0),
     ("f32", 1, 2048, 2048, 128, 128, True, 0.1),
     ("f32", 3, 77, 77, 64, 64, True, 0.0),

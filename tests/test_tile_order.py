@@ -1,12 +1,14 @@
 """Work order of the fp16 DMA kernels (xcd_map and row_window in
 csrc/sdpa_dma.h), checked on the CPU: tests/host/tile_order.hip includes the
-header, runs xcd_map on the host over a grid of batch sizes, tile counts and
-row sizes, and checks that workgroup ids map one to one onto (batch, tile),
-that each XCD owns its batch rows whole when B is a multiple of 8, that the
-tiles of a window of rows run heaviest first and rank by rank, and that the
-window is the largest divisor of B / 8 within 8 MiB of streamed rows.  The
-GPU side of the same mapping is covered by the all-batch parity checks of
-the c3/c4 configurations (B = 256 and 128) and the B = 16 / 24 edge shapes."""
+header, runs xcd_map on the host over a grid of batch sizes (multiples of 8
+and not), tile counts and chunk caps, and checks that workgroup ids map one
+to one onto (batch, tile), that each XCD covers its contiguous range of the
+batch-major tile list, that it runs that range as the fewest equal chunks of
+at most wcap rows' worth of tiles, each rank-major (heaviest tiles of all its
+rows first), that chunks are whole rows where wcap divides B / 8, and the
+row_window rule.  The GPU side of the same mapping is covered by the
+all-batch parity checks of c3/c4 (B = 256 and 128) and the B = 12, 16, 24
+and 36 edge shapes."""
 import os
 import shutil
 import subprocess

@@ -185,40 +185,78 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 
 // Workgroup id -> (batch, tile), XCD-major: ids are dealt round-robin over
 // the 8 XCDs (id % 8); XCD x owns a contiguous range of the batch-major tile
-// list, so the K/V (or Q/dO) rows a tile streams are shared in that XCD's L2
-// by the other tiles of its batch row.  Inside that range the tiles of `win`
-// consecutive batch rows are interleaved (tile-major within the window), and
-// `reverse` runs a row's tiles last-first (causal query tiles: the heaviest
-// first).  Interleaving starts the heavy tiles of all rows of a window
-// together, so the light ones fill the end of the launch; row by row, the
-// last rows' heavy tiles started late and ran alone.  win = 1 is plain row
-// order; row_window() picks it.
-__host__ __device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles, bool reverse, int win, int& b,
+// list (B tiles-long rows), so the K/V (or Q/dO) rows a tile streams are
+// shared in that XCD's L2 by the other tiles of its batch row.  The XCD
+// splits its range into the fewest chunks of at most `wcap` rows' worth of
+// tiles (equal sizes, +-1) and runs each chunk rank-major: rank 0 (the
+// heaviest tile of a row when `reverse`, which runs a row's tiles last-first)
+// of every row in the chunk, then rank 1, and so on.  The heavy tiles of a
+// chunk's rows thus start together and the light ones fill the end of the
+// launch; row by row, the last rows' heavy tiles started late and ran alone.
+// A chunk may begin or end inside a row (when B is not a multiple of 8, or
+// wcap does not divide B / 8): at each rank its rows are still a contiguous
+// interval.  wcap = 1 with whole rows per XCD is plain row order;
+// row_window() picks wcap.
+__host__ __device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles, bool reverse, int wcap, int& b,
                                                   int& t) {
     const int xcd = bid & 7, local = bid >> 3;
     const int per = nblocks >> 3, rem = nblocks & 7;
-    const int lin = xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
-    const int g = lin / (win * tiles);
-    const int k = lin - g * (win * tiles);
-    const int left = nblocks / tiles - g * win;  // rows from this window on
-    const int nr = win < left ? win : left;
-    const int r = k / nr;
-    b = g * win + (k - r * nr);
-    t = reverse ? tiles - 1 - r : r;
+    const int n_x = per + (xcd < rem ? 1 : 0);
+    const int s_x = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
+    // chunk of `local`: nch chunks, the first `extra` of them one longer
+    const int cap = wcap * tiles;
+    const int nch = (n_x + cap - 1) / cap;
+    const int base = n_x / nch, extra = n_x - base * nch;
+    int cs, size;
+    if (local < extra * (base + 1)) {
+        cs = (local / (base + 1)) * (base + 1);
+        size = base + 1;
+    } else {
+        cs = extra * (base + 1) + ((local - extra * (base + 1)) / base) * base;
+        size = base;
+    }
+    const int k = local - cs;  // position in the chunk's rank-major order
+    cs += s_x;
+    // rows r0 .. r1 of the chunk: r0 holds ranks p0 .. tiles-1, r1 ranks 0 .. p1
+    const int r0 = cs / tiles, r1 = (cs + size - 1) / tiles;
+    const int p0 = cs - r0 * tiles, p1 = cs + size - 1 - r1 * tiles;
+    int q, row;
+    if (r0 == r1) {
+        q = p0 + k;
+        row = r0;
+    } else {
+        // At rank q the rows are r0 + (q < p0) .. r1 - (q > p1), so the count
+        // is d = r1 - r0 below a = min(p0, p1 + 1) and from c = max(p0, p1 + 1)
+        // on, and d + 1 (p0 <= p1) or d - 1 (p0 > p1) in between.
+        const int d = r1 - r0;
+        const bool inner = p0 <= p1;
+        const int a = inner ? p0 : p1 + 1, c = inner ? p1 + 1 : p0;
+        const int dm = inner ? d + 1 : d - 1;
+        const int n0 = a * d, n1 = (c - a) * dm;
+        if (k < n0) {
+            q = k / d;
+            row = r0 + 1 + (k - q * d);
+        } else if (k < n0 + n1) {
+            const int kk = k - n0, j = kk / dm;
+            q = a + j;
+            row = (inner ? r0 : r0 + 1) + (kk - j * dm);
+        } else {
+            const int kk = k - n0 - n1, j = kk / d;
+            q = c + j;
+            row = r0 + (kk - j * d);
+        }
+    }
+    b = row;
+    t = reverse ? tiles - 1 - q : q;
 }
 
-// The xcd_map window for B batch rows that each stream row_bytes: the largest
-// divisor of the rows one XCD owns (B / 8) whose rows stream at most 8 MiB,
-// so windows never straddle two XCDs and their working set stays bounded; 1
-// (row order) when B is not a multiple of 8.  At B = 128 (16 rows per XCD)
-// and 2 MiB per row the c4 shape gets 4; at 0.5 MiB per row, 16.
-inline int row_window(int B, size_t row_bytes) {
-    if (B <= 0 || B % 8) return 1;
-    const int rows = B / 8;
-    int w = 1;
-    for (int d = 2; d <= rows; ++d)
-        if (rows % d == 0 && (size_t)d * row_bytes <= ((size_t)8 << 20)) w = d;
-    return w;
+// The xcd_map chunk cap for rows that each stream row_bytes: as many rows as
+// stream at most 8 MiB (at least one), so a chunk's working set stays
+// bounded.  c4 (2 MiB per row, 16 rows per XCD) gets 4; c3 (0.5 MiB, 32 rows
+// per XCD) 16.
+inline int row_window(size_t row_bytes) {
+    const size_t w = row_bytes ? ((size_t)8 << 20) / row_bytes : 1;
+    return w < 1 ? 1 : (w > (1 << 20) ? (1 << 20) : (int)w);
 }
 
 // Two fp32 values -> one dword of two RNE-rounded halves (v_cvt_pk_f16_f32).

@@ -17,7 +17,7 @@
 // Work order.  Workgroup ids are remapped so that each XCD (ids are dealt
 // round-robin over the 8 XCDs) owns whole batch rows: all tiles of a batch
 // row run on one XCD and share its L2 copy of the streamed operands; the
-// tiles of a window of rows are interleaved (xcd_map, row_window).
+// tiles of a chunk of rows are interleaved (xcd_map, row_window).
 //
 // MFMA formulation (v_mfma_f32_32x32x16_f16, fp32 accumulation; the lane
 // layouts are listed in sdpa_device.h), per group of 32 keys (lane = key):
@@ -394,7 +394,7 @@ hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream
                             const long long n = (long long)((S_kv + CK::BKV - 1) / CK::BKV) * B;
                             err = launch_kernel<sdpa_bwd_dkdv_f16_dma_kernel<DQK, DV, CA, DR>>(
                                 (unsigned)n, CK::NT, CK::LDS_BYTES, stream, p,
-                                row_window(B, (size_t)S_q * (DQK + DV) * 2));
+                                row_window((size_t)S_q * (DQK + DV) * 2));
                         }
                     }
                     return err;

@@ -491,7 +491,7 @@ hipError_t launch_bwd_dkdv_f16_split(const BwdParams& p, hipStream_t stream) {
                         const long long n = (long long)((S_kv + CS::BKV - 1) / CS::BKV) * B;
                         return launch_kernel<sdpa_bwd_dkdv_f16_split_kernel<DQK, DV, CA, DR>>(
                             (unsigned)n, CS::NT, CS::LDS_BYTES, stream, p,
-                            row_window(B, (size_t)p.s.S_q * (DQK + DV) * 2));
+                            row_window((size_t)p.s.S_q * (DQK + DV) * 2));
                     } else {
                         return hipErrorInvalidValue;  // the one-wave kernel serves D <= 64
                     }

@@ -261,7 +261,7 @@ hipError_t launch_bwd_dq_f16_dma(const BwdParams& p, hipStream_t stream) {
                     const long long n = (long long)((S_q + CQ::BM - 1) / CQ::BM) * B;
                     return launch_kernel<sdpa_bwd_dq_f16_dma_kernel<DQK, DV, CA, DR>>((unsigned)n, CQ::NT,
                                                                                 CQ::LDS_BYTES, stream, p,
-                                                                                row_window(B, (size_t)p.s.S_kv * (DQK + DV) * 2));
+                                                                                row_window((size_t)p.s.S_kv * (DQK + DV) * 2));
                 });
             });
         });

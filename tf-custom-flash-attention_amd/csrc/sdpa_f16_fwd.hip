@@ -378,7 +378,7 @@ hipError_t launch_fwd_f16_dma(const FwdParams& p, hipStream_t stream) {
                     const long long n = (long long)((S_q + Cfg::BM - 1) / Cfg::BM) * B;
                     return launch_kernel<sdpa_fwd_f16_dma_kernel<DQK, DV, decltype(c)::value, decltype(d)::value>>(
                         (unsigned)n, Cfg::NT, Cfg::LDS_BYTES, stream, p,
-                        row_window(B, (size_t)p.s.S_kv * (DQK + DV) * 2));
+                        row_window((size_t)p.s.S_kv * (DQK + DV) * 2));
                 });
             });
         });
