@@ -100,6 +100,22 @@ int main() {
                     }
                 }
         }
+    // wcap * tiles beyond 2^31 (dK/dV: a one-row query side against a long key
+    // side gives a huge cap and many key tiles)
+    for (int B : {1, 3, 9})
+        for (int T : {8192, 20000}) {
+            ++cases;
+            const int n = B * T;
+            std::vector<int> seen((size_t)n, 0);
+            for (int bid = 0; bid < n; ++bid) {
+                int b = -1, t = -1;
+                sdpa::xcd_map(bid, n, T, false, 1 << 20, b, t);
+                const bool ok = b >= 0 && b < B && t >= 0 && t < T;
+                CHECK(ok, "huge cap B=%d T=%d bid=%d -> (%d,%d)", B, T, bid, b, t);
+                if (ok) ++seen[(size_t)b * T + t];
+            }
+            for (int i = 0; i < n; ++i) CHECK(seen[i] == 1, "huge cap B=%d T=%d tile %d seen %d", B, T, i, seen[i]);
+        }
     if (fails) {
         std::printf("%d failures over %d cases\n", fails, cases);
         return 1;

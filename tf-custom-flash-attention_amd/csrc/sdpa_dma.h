@@ -203,9 +203,11 @@ __host__ __device__ __forceinline__ void xcd_map(int bid, int nblocks, int tiles
     const int per = nblocks >> 3, rem = nblocks & 7;
     const int n_x = per + (xcd < rem ? 1 : 0);
     const int s_x = xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per;
-    // chunk of `local`: nch chunks, the first `extra` of them one longer
-    const int cap = wcap * tiles;
-    const int nch = (n_x + cap - 1) / cap;
+    // chunk of `local`: nch chunks, the first `extra` of them one longer (the
+    // cap in 64 bits: a one-row side against a long other side makes
+    // wcap * tiles exceed 2^31)
+    const long long cap = (long long)wcap * tiles;
+    const int nch = cap >= n_x ? 1 : (n_x + (int)cap - 1) / (int)cap;
     const int base = n_x / nch, extra = n_x - base * nch;
     int cs, size;
     if (local < extra * (base + 1)) {
