@@ -4,6 +4,8 @@
 Gates (north_star): fp32 o/grads within 1e-5 max-abs; fp16 o within 2e-3 and
 gradients within 1e-2 of the oracle instantiated in fp32 on the fp16-exact
 inputs; dropout masks bit-exact (test_dropout_gpu.py)."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -157,6 +159,18 @@ EDGE = [
     ("f32", 1, 50, 50, 1, 3, True, 0.0),
     ("f32", 2, 96, 64, 128, 8, False, 0.5),
 ]
+
+
+# Several work-order chunks per XCD that begin and end inside batch rows: at
+# B = 36 and S = 4096 (D = 128, so 2 MiB of K/V per row and a 4-row chunk cap)
+# each XCD owns 4.5 rows and runs them as two chunks of 2.25 rows.  Two
+# batches in full against the oracle, every batch on the row subset.
+CHUNKED = Cfg("b36_f16_chunks", "f16", 36, 4096, 4096, 128, 128, True, 0.1, 1 / math.sqrt(128), 5, 3,
+              check_batches=(0, 35))
+
+
+def test_chunked_work_order(pkg, O):
+    run_and_check(pkg, O, CHUNKED)
 
 
 @pytest.mark.parametrize("case", EDGE, ids=["-".join(map(str, e)) for e in EDGE])
