@@ -149,7 +149,11 @@ EDGE = [
     # batch row (1.5 and 4.5 rows per XCD), run rank-major as one chunk
     ("f16", 12, 1024, 1024, 64, 64, True, 0.0),
     ("f16", 36, 384, 384, 128, 128, True, 0.1),
+    # the register-staged kernels' order (id % B, heaviest level first) with
+    # B not a multiple of 8: fp16 at D = 124 and fp32
+    ("f16", 12, 512, 512, 124, 124, True, 0.1),
     ("f32", 2, 1, 1, 8, 8, False, 0.0),
+    ("f32", 12, 512, 512, 128, 128, True, 0.1),
     ("f32", 1, 2048, 2048, 128, 128, True, 0.1),
     ("f32", 3, 77, 77, 64, 64, True, 0.0),
     ("f32", 2, 129, 200, 128, 128, False, 0.3),
