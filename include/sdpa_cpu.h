@@ -15,7 +15,8 @@
  * pointers.  nthreads <= 0 uses every hardware thread.
  *
  * Semantics of the reference CPU functors: dropout is active iff p > 0
- * (sdpa_cpu.cc:232-235), the backward skips an element iff P < 1e-6
+ * (sdpa_cpu.cc:232-235), p > 1 drops every element, p == 1 is rejected
+ * (SDPA_ERR_DROPOUT_RANGE), the backward skips an element iff P < 1e-6
  * (sdpa_cpu.cc:384-385); products and accumulations run in fp32 (the
  * reference rounds half*half products and dK/dV to half, sdpa_cpu.cc:261,
  * 416-417; the results agree to within the fp16 tolerances).

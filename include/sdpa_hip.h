@@ -97,7 +97,10 @@ int sdpa_hip_check_bwd(int q_rank, const int64_t* q_shape, int k_rank, const int
  * o     = softmax(scale * q k^T [causal]) (dropout) v     [B,S_q,D_v], dtype
  * stats = m + log(l + 1e-6)                               [B,S_q] fp32
  * Requires max(D_qk, D_v) <= 128 and, with causal_mask, S_q == S_kv.
- * dropout must be < 1 (values <= 1e-6 disable dropout, as the reference GPU).  */
+ * dropout <= 1e-6 disables dropout (as the reference GPU); dropout > 1 drops
+ * every element as the reference does (o = 0, the usual stats; in the
+ * backward dV = 0 and dS = -P delta); dropout == 1 returns
+ * SDPA_ERR_DROPOUT_RANGE (the reference would scale by 1 / 0).  */
 int sdpa_hip_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* stats,
                  int B, int S_q, int S_kv, int D_qk, int D_v, float scale, float dropout,
                  int causal_mask, uint64_t seed, uint64_t offset, hipStream_t stream);

@@ -146,7 +146,8 @@ def test_launch_entry_points_reject_before_device_work(pkg):
     assert fwd(1, -1, 4, 4, 8, 8, 0.0, 0) == 19         # negative dim
     assert fwd(1, 1, 4, 5, 8, 8, 0.0, 1) == 15          # causal with S_q != S_kv
     assert fwd(1, 1, 4, 4, 8, 129, 0.0, 0) == 16        # feature size over 128
-    assert fwd(1, 1, 4, 4, 8, 8, 1.0, 0) == 21          # dropout >= 1
+    assert fwd(1, 1, 4, 4, 8, 8, 1.0, 0) == 21          # dropout == 1
+    assert fwd(1, 1, 4, 4, 8, 8, 1.5, 0) == 20          # dropout > 1 passes the checks (drops all)
     assert fwd(1, 0, 4, 4, 8, 8, 0.0, 0) == 0           # empty: nothing to do
     assert fwd(1, 1, 4, 4, 8, 8, 0.0, 0) == 20          # null pointers for non-empty tensors
     bwd = lambda ws_bytes: L.sdpa_hip_bwd(1, null, null, null, null, null, null, null, null, null,

@@ -91,3 +91,27 @@ def test_host_kernels_thread_count_invariant(host):
     for other in outs[1:]:
         for a, b in zip(outs[0], other):
             assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_host_kernels_dropout_above_one(host, O, pkg, dtype):
+    """dropout > 1 drops every element, as in the reference (u <= 1 < p): o = 0,
+    the usual statistics, dV = 0 and dS = -P delta for every element (the
+    backward is run on an o that is not 0, so delta != 0).  dropout == 1 is
+    rejected (the reference would scale the rare u == 1 elements by 1 / 0)."""
+    c = Cfg("above_one", dtype, 2, 70, 70, 48, 24, True, 1.5, 0.2, 3, 5)
+    q, k, v, d_o = make_inputs(c)
+    kw = dict(scale=c.scale, dropout=c.dropout, causal_mask=c.causal, seed=c.seed, offset=c.offset)
+    o, s = host.sdpa(q, k, v, **kw)
+    o_ref, s_ref = O.sdpa_fwd_gate(q, k, v, gpu_gates=False, **kw)
+    assert np.all(o == 0) and np.all(o_ref == 0)
+    assert maxabs(s, s_ref) <= TOL[dtype]["stats"]
+    o_in, _ = host.sdpa(q, k, v, **dict(kw, dropout=0.0))
+    g = host.sdpa_grad(q, k, v, o_in, s, d_o, **kw)
+    g_ref = O.sdpa_bwd_gate(q, k, v, o_in, s, d_o, gpu_gates=False, **kw)
+    assert np.all(g[2] == 0)
+    for name, a, r in zip(("dq", "dk", "dv"), g, g_ref):
+        assert maxabs(a, r) <= TOL[dtype]["grad"], name
+    assert np.abs(g_ref[0].astype(np.float32)).max() > 1e-2
+    with pytest.raises(pkg.InvalidArgumentError, match="dropout must not be 1"):
+        host.sdpa(q, k, v, **dict(kw, dropout=1.0))

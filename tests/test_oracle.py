@@ -236,3 +236,47 @@ def test_gpu_and_cpu_gates_differ_only_below_1e6(O):
     a = O.sdpa_fwd(q, k, v, dropout=5e-7, seed=1, offset=2, gpu_gates=True)
     b = O.sdpa_fwd(q, k, v, dropout=5e-7, seed=1, offset=2, gpu_gates=False)
     assert not np.array_equal(a[0], b[0])  # CPU rescales by 1/(1-p) != 1
+
+
+def _drop_all_closed_form(q, k, v, o, d_o, scale, causal):
+    """float64 closed form of the reference with every element dropped
+    (dropout > 1: u <= 1 < p; sdpa/sdpa_cpu.cc:274-285, 393-409):
+    o = 0, stats as without dropout, dS = -P delta scale, dV = 0."""
+    q, k, v, o, d_o = (a.astype(np.float64) for a in (q, k, v, o, d_o))
+    s = scale * np.einsum("bid,bjd->bij", q, k)
+    if causal:
+        s = np.where(np.tril(np.ones(s.shape[1:], bool))[None], s, -np.inf)
+    m = s.max(-1, keepdims=True)
+    p = np.exp(s - m)
+    l = p.sum(-1, keepdims=True)
+    stats = (m + np.log(l + 1e-6))[..., 0]
+    P = np.exp(s - stats[..., None])
+    P = np.where(P < 1e-6, 0.0, P)                      # the backward's skip (sdpa_cpu.cc:384-385)
+    delta = (d_o * o).sum(-1)                           # D_i (sdpa_cpu.cc:359-364)
+    ds = -P * delta[..., None] * scale
+    dq = np.einsum("bij,bjd->bid", ds, k)
+    dk = np.einsum("bij,bid->bjd", ds, q)
+    return stats, dq, dk, np.zeros(v.shape)
+
+
+@pytest.mark.parametrize("gpu_gates", [True, False])
+@pytest.mark.parametrize("causal", [False, True])
+def test_oracle_dropout_above_one(O, gpu_gates, causal):
+    """dropout > 1 drops every element in the reference: o = 0, stats as
+    without dropout, dV = 0, dQ / dK from dS = -P delta.  The backward is run
+    on an o that is not 0 (the reference takes o as given), so delta != 0."""
+    rng = np.random.default_rng(5)
+    B, S, Dq, Dv, scale = 2, 24, 16, 8, 0.3
+    q, k = (rng.standard_normal((B, S, Dq)).astype(np.float32) for _ in range(2))
+    v, o_in, d_o = (rng.standard_normal((B, S, Dv)).astype(np.float32) for _ in range(3))
+    kw = dict(scale=scale, dropout=1.5, causal_mask=causal, seed=3, offset=9, gpu_gates=gpu_gates)
+    o, s = O.sdpa_fwd(q, k, v, **kw)
+    assert np.all(o == 0)
+    stats, dq_ref, dk_ref, dv_ref = _drop_all_closed_form(q, k, v, o_in, d_o, scale, causal)
+    assert np.abs(s - stats).max() < 1e-5
+    _, s0 = O.sdpa_fwd(q, k, v, **dict(kw, dropout=0.0))
+    assert np.abs(s - s0).max() == 0                   # l sums the undropped probabilities
+    dq, dk, dv = O.sdpa_bwd(q, k, v, o_in, s, d_o, **kw)
+    assert np.all(dv == 0)
+    assert np.abs(dq - dq_ref).max() < 1e-5 and np.abs(dk - dk_ref).max() < 1e-5
+    assert np.abs(dq).max() > 0.1                      # not trivially zero

@@ -417,3 +417,45 @@ def test_gate_threshold_elements(pkg, O, dt, D, p):
         assert min(sep_lo, sep_hi) > 4 * TOL["f16"]["grad"]
         assert maxabs(g[1], ref1[1]) <= tol
         assert min(maxabs(g[1], lo[1]), maxabs(g[1], hi[1])) > 3 * TOL["f16"]["grad"]
+
+
+ABOVE_ONE = [
+    Cfg("above1_f16_d128_causal", "f16", 2, 200, 200, 128, 128, True, 1.5, 128 ** -0.5, 7, 3),
+    Cfg("above1_f16_d64_causal", "f16", 2, 150, 150, 64, 64, True, 2.0, 0.125, 7, 3),
+    Cfg("above1_f16_d124_cross", "f16", 2, 90, 140, 124, 60, False, 1.25, 0.09, 1, 2),
+    Cfg("above1_f32_d128_64", "f32", 2, 70, 130, 128, 64, False, 1.5, 128 ** -0.5, 5, 6),
+    Cfg("above1_f32_d32_4", "f32", 3, 40, 40, 32, 4, True, 3.0, 32 ** -0.5, 9, 1),
+]
+
+
+@pytest.mark.parametrize("c", ABOVE_ONE, ids=[c.name for c in ABOVE_ONE])
+def test_dropout_above_one(pkg, O, c):
+    """dropout > 1 drops every element, as in the reference (u <= 1 < p;
+    sdpa/sdpa_fwd.cu.cc:136-146, sdpa/sdpa_bwd.cu.cc:135-157): o = 0 with the
+    usual statistics, dV = 0, and dS = -P delta for every element.  The
+    backward is run on the o of a dropout-free forward, so delta != 0 and dQ /
+    dK are not trivially 0.  Covers the DMA kernels at 128 (split dK/dV) and 64
+    (one-wave dK/dV), the register-staged fp16 kernels (D = 124) and fp32."""
+    q, k, v, d_o = make_inputs(c)
+    tol = TOL[c.dtype]
+    kw = dict(dropout=c.dropout, scale=c.scale, causal_mask=c.causal)
+    print(f"[case] {c.name} p={c.dropout}", flush=True)
+    o, s = pkg.sdpa(_t(q), _t(k), _t(v), c.seed, c.offset, **kw)
+    o0, _ = pkg.sdpa(_t(q), _t(k), _t(v), c.seed, c.offset, **dict(kw, dropout=0.0))
+    dq, dk, dv = pkg.sdpa_grad(_t(q), _t(k), _t(v), o0, s, _t(d_o), c.seed, c.offset, **kw)
+    torch.cuda.synchronize()
+    o_h, s_h, o0_h = _np(o), _np(s), _np(o0)
+    okw = oracle_kw(c, 0)
+    o_ref, s_ref = O.sdpa_fwd_gate(q, k, v, **okw)
+    assert np.all(o_h == 0) and np.all(o_ref == 0)
+    assert maxabs(s_h, s_ref) <= tol["stats"]
+    g_ref = O.sdpa_bwd_gate(q, k, v, o0_h, s_h, d_o, **okw)
+    g = (_np(dq), _np(dk), _np(dv))
+    assert np.all(g[2] == 0)
+    errs = {n: maxabs(a, r) for n, a, r in zip(("dq", "dk", "dv"), g, g_ref)}
+    print(f"[errs] {c.name}: " + " ".join(f"{k}={v:.3e}" for k, v in errs.items()), flush=True)
+    assert np.abs(g_ref[0].astype(np.float32)).max() > 1e-2
+    for n, e in errs.items():
+        assert e <= tol["grad"], (n, errs)
+    with pytest.raises(pkg.InvalidArgumentError, match="dropout must not be 1"):
+        pkg.sdpa(_t(q), _t(k), _t(v), c.seed, c.offset, **dict(kw, dropout=1.0))

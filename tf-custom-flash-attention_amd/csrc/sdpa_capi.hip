@@ -42,13 +42,27 @@ uint64_t drop_threshold_impl(float p) {
 
 // Host-side derivation of the per-call constants (reference:
 // dp_inverse = 1 / (1 - p) when p > EPSF, sdpa/sdpa_fwd.cu.cc:20).
-sdpa::AttnScalars make_scalars(float scale, float dropout, int causal, uint64_t seed, uint64_t offset) {
+// dropout > 1 drops every element in the reference (u <= 1 < p,
+// sdpa/sdpa_fwd.cu.cc:136-146, sdpa/sdpa_bwd.cu.cc:135-157): o = 0 with the
+// usual statistics (l sums the undropped probabilities), dV = 0 and
+// dS = -P delta everywhere.  Here that is keep_scale = 0: the forward runs
+// without dropout and scales o by 0; the backward runs with dropout, where
+// every kernel forms dS = P (keep ? dP keep_scale - delta : -delta), i.e.
+// -P delta for kept and dropped elements alike, and scales dV by keep_scale.
+sdpa::AttnScalars make_scalars(float scale, float dropout, int causal, uint64_t seed, uint64_t offset,
+                               bool backward) {
     sdpa::AttnScalars c{};
     c.scale = scale;
     c.scale_log2 = scale * sdpa::kLog2e;
-    c.use_dropout = dropout > sdpa::kEps ? 1 : 0;
-    c.keep_scale = c.use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
-    c.drop_threshold = c.use_dropout ? (uint32_t)drop_threshold_impl(dropout) : 0u;
+    if (dropout > 1.0f) {
+        c.use_dropout = backward ? 1 : 0;
+        c.keep_scale = 0.0f;
+        c.drop_threshold = 0xFFFFFFFFu;  // immaterial with keep_scale = 0
+    } else {
+        c.use_dropout = dropout > sdpa::kEps ? 1 : 0;
+        c.keep_scale = c.use_dropout ? 1.0f / (1.0f - dropout) : 1.0f;
+        c.drop_threshold = c.use_dropout ? (uint32_t)drop_threshold_impl(dropout) : 0u;
+    }
     c.causal = causal ? 1 : 0;
     c.seed_offset = seed + offset;
     return c;
@@ -59,7 +73,7 @@ int check_common(int dtype, int B, int S_q, int S_kv, int D_qk, int D_v, float d
     if (B < 0 || S_q < 0 || S_kv < 0 || D_qk < 0 || D_v < 0) return SDPA_ERR_NEGATIVE_DIM;
     if (causal && S_q != S_kv) return SDPA_ERR_CAUSAL_SEQ;
     if ((D_qk > D_v ? D_qk : D_v) > 128) return SDPA_ERR_FEATURE_TOO_LARGE;
-    if (!(dropout < 1.0f) && !isnan(dropout)) return SDPA_ERR_DROPOUT_RANGE;
+    if (dropout == 1.0f) return SDPA_ERR_DROPOUT_RANGE;  // the reference divides by 1 - p
     return SDPA_OK;
 }
 
@@ -72,13 +86,17 @@ bool vec_ok(int dtype, int D_qk, int D_v, std::initializer_list<const void*> ptr
 }
 
 // keep[b, i, j] from the same hash code the attention kernels use.
+// use_dropout: 0 keeps every element, 1 applies the hash test, 2 drops every
+// element (dropout > 1).
 __global__ void dropout_mask_kernel(uint8_t* keep, int B, int S_q, int S_kv, int use_dropout,
                                     uint32_t thr, uint64_t seed_offset) {
     const uint64_t total = (uint64_t)B * S_q * S_kv;
     for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (uint64_t)gridDim.x * blockDim.x) {
         const uint64_t row = idx / (uint64_t)S_kv, j = idx % (uint64_t)S_kv;
-        keep[idx] = use_dropout ? (uint8_t)sdpa::lcg_keep(sdpa::lcg_state(seed_offset, row, S_kv, j), thr) : 1;
+        keep[idx] = use_dropout == 2 ? 0
+                    : use_dropout ? (uint8_t)sdpa::lcg_keep(sdpa::lcg_state(seed_offset, row, S_kv, j), thr)
+                                  : 1;
     }
 }
 
@@ -111,7 +129,7 @@ const char* sdpa_hip_status_string(int status) {
         case SDPA_ERR_DTYPE: return "dtype must be float16 or float32";
         case SDPA_ERR_NEGATIVE_DIM: return "tensor dimensions must be non-negative";
         case SDPA_ERR_NULL_POINTER: return "null device pointer for a non-empty tensor";
-        case SDPA_ERR_DROPOUT_RANGE: return "dropout must be < 1";
+        case SDPA_ERR_DROPOUT_RANGE: return "dropout must not be 1 (the kept elements would be scaled by 1 / (1 - p))";
         case SDPA_ERR_WORKSPACE: return "backward workspace is too small";
         case SDPA_ERR_HIP: return "HIP runtime error";
         case SDPA_ERR_SCRATCH_LIMIT:
@@ -178,7 +196,7 @@ int sdpa_hip_fwd(int dtype, const void* q, const void* k, const void* v, void* o
     p.o = o;
     p.stats = stats;
     p.s = sdpa::AttnShape{B, S_q, S_kv, D_qk, D_v};
-    p.c = make_scalars(scale, dropout, causal_mask, seed, offset);
+    p.c = make_scalars(scale, dropout, causal_mask, seed, offset, false);
     const bool vec = vec_ok(dtype, D_qk, D_v, {q, k, v, o});
     if (dtype == SDPA_DTYPE_F16 && vec) return hip_status(sdpa::launch_fwd_f16_dma(p, stream));
     return hip_status(sdpa::launch_fwd(p, (sdpa::DType)dtype, vec, stream));
@@ -224,7 +242,7 @@ int bwd_entry(int phases, int dtype, const void* q, const void* k, const void* v
     p.stats2 = static_cast<float*>(workspace);
     p.delta = static_cast<float*>(workspace) + (size_t)B * S_q;
     p.s = sdpa::AttnShape{B, S_q, S_kv, D_qk, D_v};
-    p.c = make_scalars(scale, dropout, causal_mask, seed, offset);
+    p.c = make_scalars(scale, dropout, causal_mask, seed, offset, true);
     const bool vec = vec_ok(dtype, D_qk, D_v,
                             {q, k, v, d_o, want_dq ? o : nullptr, want_dq ? dq : nullptr,
                              want_kv ? dk : nullptr, want_kv ? dv : nullptr});
@@ -327,15 +345,17 @@ uint64_t sdpa_hip_drop_threshold(float dropout) { return drop_threshold_impl(dro
 int sdpa_hip_dropout_mask(uint8_t* keep, int B, int S_q, int S_kv, float dropout, uint64_t seed,
                           uint64_t offset, hipStream_t stream) {
     if (B < 0 || S_q < 0 || S_kv < 0) return SDPA_ERR_NEGATIVE_DIM;
-    if (!(dropout < 1.0f) && !isnan(dropout)) return SDPA_ERR_DROPOUT_RANGE;
+    if (dropout == 1.0f) return SDPA_ERR_DROPOUT_RANGE;
     const uint64_t total = (uint64_t)B * S_q * S_kv;
     if (total == 0) return SDPA_OK;
     if (!keep) return SDPA_ERR_NULL_POINTER;
-    const sdpa::AttnScalars c = make_scalars(1.0f, dropout, 0, seed, offset);
+    const sdpa::AttnScalars c = make_scalars(1.0f, dropout, 0, seed, offset, false);
     const uint64_t blocks = (total + 255) / 256;
     const unsigned grid = (unsigned)(blocks < 65536 ? blocks : 65536);
+    // dropout > 1: every element dropped (use_dropout with an all-dropping test)
+    const bool all = dropout > 1.0f;
     hipLaunchKernelGGL(dropout_mask_kernel, dim3(grid), dim3(256), 0, stream, keep, B, S_q, S_kv,
-                       c.use_dropout, c.drop_threshold, c.seed_offset);
+                       all ? 2 : c.use_dropout, c.drop_threshold, c.seed_offset);
     return hip_status(hipGetLastError());
 }
 

@@ -139,7 +139,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
         auto land_block = [&](int m) {
             if (PCOPY && m < nsteps) {
                 wait_vm();
-                if (DROP && kw == 1) {
+                if (DROP && kw == 1 && p.c.keep_scale != 0.f) {
                     float* dl = reinterpret_cast<float*>(smem + (m % NSTAGE) * Cfg::STAGE + Cfg::QB + Cfg::OB) + BQ;
                     dl[lane] = dl[lane] / p.c.keep_scale;
                 }
@@ -341,6 +341,14 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
         // dK is stored with scale / (1-p).  Each block's delta row is
         // rewritten as delta' in LDS once, by the wave that copies it.
         const float ksc = p.c.keep_scale;
+        // keep_scale = 0 (dropout > 1: every element dropped in the reference,
+        // dS = -P delta): dP is formed from zero V rows, delta is not rescaled
+        // and dK is stored with scale, so dS' = -|x| delta for every element.
+        const bool drop_all = DROP && ksc == 0.f;
+        if (drop_all) {
+#pragma unroll
+            for (int ks = 0; ks < DV / 16; ++ks) vreg[ks] = half8{};
+        }
         const float* st2b = p.stats2 + (size_t)b * S_q;
         const float* deltab = p.delta + (size_t)b * S_q;
         TileDma<BQ, LQ, 4> qd;
@@ -453,7 +461,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
             }
             // block n has landed: its delta row becomes delta' (read by this
             // role from the next step on; the P role never reads it)
-            if (DROP && kw == 1 && n < nsteps) {
+            if (DROP && kw == 1 && n < nsteps && !drop_all) {
                 float* dl = reinterpret_cast<float*>(smem + (n % NSTAGE) * Cfg::STAGE + Cfg::QB + Cfg::OB) + BQ;
                 dl[lane] = dl[lane] / ksc;
             }
@@ -468,7 +476,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
         }
         if (key_ok) {
             half_t* dKb = static_cast<half_t*>(p.dk) + ((size_t)b * S_kv + my_k) * D_qk;
-            const float fk = DROP ? p.c.scale * ksc : p.c.scale;
+            const float fk = DROP && !drop_all ? p.c.scale * ksc : p.c.scale;
             if (D_qk == DQK) store_rows_f16<DQK>(dKb, dkacc, fk, hh);
             else store_rows_f16_n<DQK>(dKb, dkacc, fk, hh, D_qk);
         }

@@ -317,7 +317,9 @@ int check(int dtype, int B, int S_q, int S_kv, int D_qk, int D_v, float dropout,
     if (B < 0 || S_q < 0 || S_kv < 0 || D_qk < 0 || D_v < 0) return SDPA_ERR_NEGATIVE_DIM;
     if (causal && S_q != S_kv) return SDPA_ERR_CAUSAL_SEQ;
     if (std::max(D_qk, D_v) > DMAX) return SDPA_ERR_FEATURE_TOO_LARGE;
-    if (!(dropout < 1.0f) && !std::isnan(dropout)) return SDPA_ERR_DROPOUT_RANGE;
+    // dropout > 1 drops every element (u <= 1 < p), as in the reference; at
+    // dropout == 1 the reference scales the rare u == 1 elements by 1 / 0
+    if (dropout == 1.0f) return SDPA_ERR_DROPOUT_RANGE;
     return SDPA_OK;
 }
 
