@@ -6,6 +6,10 @@
   sdpa_kernels.cc registers both ops for DEVICE_CPU and DEVICE_GPU x
   {float, half} with seed / offset in host memory on the GPU
   (sdpa/sdpa_cpu.cc:460-488).
+* Without TensorFlow: sdpa.py runs against a stand-in tensorflow module that
+  records the library it loads, the forward call and the gradient's SdpaGrad
+  call (inputs, attributes, return arity), as the reference wires them
+  (test.py:12-30); planted wiring mistakes fail that check.
 * With TensorFlow: build.sh builds sdpa_rocm.so, sdpa.py loads it, and the
   op plus its registered gradient agree with the oracle on the CPU and, on a
   GPU, with the oracle at the north_star tolerances.  TensorFlow is not
@@ -133,3 +137,106 @@ def test_tf_op_gpu(tf_sdpa, O, c):
     assert maxabs(o, o_ref) <= TOL[c.dtype]["o"]
     for g, r in zip(grads, O.sdpa_bwd_gate(q, k, v, o, s, d_o, **oracle_kw(c))):
         assert maxabs(g, r) <= TOL[c.dtype]["grad"]
+
+
+# ---- sdpa.py executed against a stand-in TensorFlow module -------------------
+# TensorFlow is absent here, so the module's wiring is checked by running it
+# against a recorder: the library it loads, the forward call, and the
+# registered gradient's call of SdpaGrad (inputs, attributes, return arity),
+# as the reference wires them (test.py:12-30, README.md:28-56).
+
+class _Recorder:
+    """The loaded op library: records every call, returns sentinels."""
+
+    def __init__(self):
+        self.calls = []
+
+    def sdpa(self, *args, **kwargs):
+        self.calls.append(("sdpa", args, kwargs))
+        return ("o", "stats")
+
+    def sdpa_grad(self, *args, **kwargs):
+        self.calls.append(("sdpa_grad", args, kwargs))
+        return ("dq", "dk", "dv")
+
+
+def _fake_tensorflow():
+    import types
+    tf = types.ModuleType("tensorflow")
+    tf.Tensor, tf.Operation = object, object
+    tf.loaded, tf.gradients, tf.lib = [], {}, _Recorder()
+
+    def load_op_library(path):
+        tf.loaded.append(path)
+        return tf.lib
+
+    def RegisterGradient(name):
+        def deco(fn):
+            tf.gradients[name] = fn
+            return fn
+        return deco
+
+    tf.load_op_library, tf.RegisterGradient = load_op_library, RegisterGradient
+    return tf
+
+
+class _FakeOp:
+    """An Sdpa op as the gradient function sees it."""
+
+    def __init__(self, inputs, outputs, attrs):
+        self.inputs, self.outputs, self._attrs = inputs, outputs, attrs
+
+    def get_attr(self, name):
+        return self._attrs[name]
+
+
+def _check_sdpa_module(path, monkeypatch):
+    """Run the module at `path` against the stand-in and assert the
+    reference's wiring; AssertionError on any difference."""
+    tf = _fake_tensorflow()
+    monkeypatch.setitem(__import__("sys").modules, "tensorflow", tf)
+    monkeypatch.delenv("SDPA_ROCM_LIB", raising=False)
+    spec = importlib.util.spec_from_file_location("sdpa_tf_module_under_test", path)
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    assert tf.loaded == [os.path.join(os.path.dirname(path), "sdpa_rocm.so")]
+    # forward: the op's positional inputs and keyword attributes, its outputs returned
+    q, k, v, seed, offset = (object() for _ in range(5))
+    assert m.sdpa(q, k, v, seed, offset, dropout=0.25, scale=0.125, causal_mask=True) == ("o", "stats")
+    assert tf.lib.calls[-1] == ("sdpa", (q, k, v, seed, offset),
+                                dict(dropout=0.25, scale=0.125, causal_mask=True))
+    # the gradient registered for "Sdpa": SdpaGrad(q, k, v, o, stats, d_o, seed, offset)
+    assert set(tf.gradients) == {"Sdpa"}
+    o, stats, d_o, d_stats = (object() for _ in range(4))
+    attrs = dict(dropout=0.3, scale=0.5, causal_mask=True)
+    op = _FakeOp((q, k, v, seed, offset), (o, stats), attrs)
+    grads = tf.gradients["Sdpa"](op, d_o, d_stats)
+    assert tuple(grads) == ("dq", "dk", "dv", None, None)
+    assert tf.lib.calls[-1] == ("sdpa_grad", (q, k, v, o, stats, d_o, seed, offset), attrs)
+    # the library path can be overridden
+    monkeypatch.setenv("SDPA_ROCM_LIB", "/elsewhere/sdpa_rocm.so")
+    tf.loaded.clear()
+    spec.loader.exec_module(importlib.util.module_from_spec(spec))
+    assert tf.loaded == ["/elsewhere/sdpa_rocm.so"]
+
+
+def test_sdpa_module_wiring_with_stand_in_tensorflow(monkeypatch):
+    _check_sdpa_module(os.path.join(TF_OP, "sdpa.py"), monkeypatch)
+
+
+@pytest.mark.parametrize("old,new", [
+    ("o, stats = op.outputs", "stats, o = op.outputs"),                        # o and stats swapped
+    ("d_o, seed, offset,", "d_o, offset, seed,"),                              # seed and offset swapped
+    ("causal_mask=op.get_attr(\"causal_mask\"))", "causal_mask=False)"),       # attribute dropped
+    ("return dq, dk, dv, None, None", "return dq, dk, dv, None"),              # wrong arity
+    ("dropout=op.get_attr(\"dropout\"), scale=op.get_attr(\"scale\")",
+     "dropout=op.get_attr(\"scale\"), scale=op.get_attr(\"dropout\")"),       # attributes crossed
+    ("return mod.sdpa(q, k, v, seed, offset,", "return mod.sdpa(q, k, v, offset, seed,"),
+])
+def test_sdpa_module_check_catches_planted_mistakes(tmp_path, monkeypatch, old, new):
+    src = open(os.path.join(TF_OP, "sdpa.py")).read()
+    assert old in src
+    planted = tmp_path / "sdpa.py"
+    planted.write_text(src.replace(old, new))
+    with pytest.raises(AssertionError):
+        _check_sdpa_module(str(planted), monkeypatch)
