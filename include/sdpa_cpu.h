@@ -34,6 +34,22 @@ extern "C" {
 #define SDPA_CPU_DTYPE_F32 0
 #define SDPA_CPU_DTYPE_F16 1
 
+/* Message for a status code (static storage, never NULL); the same codes and
+ * messages as sdpa_hip_status_string, without the GPU library. */
+const char* sdpa_cpu_status_string(int status);
+
+/* The reference's argument checks of Sdpa / SdpaGrad, as sdpa_hip_check_fwd
+ * and sdpa_hip_check_bwd (sdpa/sdpa_ops.cc:22-25,55-57,
+ * sdpa/sdpa_cpu.cc:37-69,116-168): shapes as rank + dims, scalars rank 0;
+ * the first failing check in the reference's order. */
+int sdpa_cpu_check_fwd(int q_rank, const int64_t* q_shape, int k_rank, const int64_t* k_shape, int v_rank,
+                       const int64_t* v_shape, int seed_rank, int offset_rank, int causal_mask);
+
+int sdpa_cpu_check_bwd(int q_rank, const int64_t* q_shape, int k_rank, const int64_t* k_shape, int v_rank,
+                       const int64_t* v_shape, int o_rank, const int64_t* o_shape, int stats_rank,
+                       const int64_t* stats_shape, int do_rank, const int64_t* do_shape, int seed_rank,
+                       int offset_rank, int causal_mask);
+
 int sdpa_cpu_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* stats,
                  int B, int S_q, int S_kv, int D_qk, int D_v, float scale, float dropout,
                  int causal_mask, uint64_t seed, uint64_t offset, int nthreads);

@@ -115,3 +115,41 @@ def test_host_kernels_dropout_above_one(host, O, pkg, dtype):
     assert np.abs(g_ref[0].astype(np.float32)).max() > 1e-2
     with pytest.raises(pkg.InvalidArgumentError, match="dropout must not be 1"):
         host.sdpa(q, k, v, **dict(kw, dropout=1.0))
+
+
+def test_host_binding_checks_before_reading(host, pkg, monkeypatch):
+    """The numpy binding runs the op's checks (sdpa/sdpa_cpu.cc:37-69,
+    116-168) and the dtype rules before any data is read, through
+    libsdpa_cpu.so alone: the GPU library is made unloadable here."""
+    monkeypatch.setattr(pkg, "LIB_PATH", "/nonexistent/libsdpa_hip.so")
+    monkeypatch.setattr(pkg, "_lib", None)
+    f = lambda *s, dt=np.float32: np.zeros(s, dt)
+    E = pkg.InvalidArgumentError
+    with pytest.raises(E, match="K batch size mismatch"):      # q [4,16,8] against k, v [1,16,8]
+        host.sdpa(f(4, 16, 8), f(1, 16, 8), f(1, 16, 8))
+    with pytest.raises(E, match="K feature size mismatch"):
+        host.sdpa(f(2, 16, 8), f(2, 16, 6), f(2, 16, 8))
+    with pytest.raises(E, match="V seq size mismatch"):
+        host.sdpa(f(2, 16, 8), f(2, 16, 8), f(2, 15, 8))
+    with pytest.raises(E, match="rank 3"):
+        host.sdpa(f(16, 8), f(16, 8), f(16, 8))
+    with pytest.raises(E, match="seed must be scalar"):
+        host.sdpa(f(2, 4, 8), f(2, 4, 8), f(2, 4, 8), seed=np.array([1, 2]))
+    with pytest.raises(E, match="k has dtype float16"):
+        host.sdpa(f(2, 4, 8), f(2, 4, 8, dt=np.float16), f(2, 4, 8))
+    with pytest.raises(E, match="T must be half or float"):
+        host.sdpa(f(2, 4, 8, dt=np.float64), f(2, 4, 8, dt=np.float64), f(2, 4, 8, dt=np.float64))
+    q, kv, o, s = f(2, 4, 8), f(2, 6, 8), f(2, 4, 8), f(2, 4)
+    with pytest.raises(E, match="O seq size mismatch"):
+        host.sdpa_grad(q, kv, kv, f(2, 5, 8), s, o)
+    with pytest.raises(E, match="dO feature size mismatch"):
+        host.sdpa_grad(q, kv, kv, o, s, f(2, 4, 7))
+    with pytest.raises(E, match="S batch size mismatch"):
+        host.sdpa_grad(q, kv, kv, o, f(3, 4), o)
+    with pytest.raises(E, match="stats must be float32"):
+        host.sdpa_grad(q, kv, kv, o, s.astype(np.float16), o)
+    with pytest.raises(E, match="d_o has dtype float16"):
+        host.sdpa_grad(q, kv, kv, o, s, o.astype(np.float16))
+    with pytest.raises(E, match="dropout must not be 1"):        # a kernel-side check, same messages
+        host.sdpa(f(2, 4, 8), f(2, 4, 8), f(2, 4, 8), dropout=1.0)
+    assert pkg._lib is None  # the GPU library was never loaded

@@ -33,6 +33,7 @@
 #include <thread>
 #include <vector>
 
+#include "sdpa_checks.h"
 #include "sdpa_cpu.h"
 #include "sdpa_hip.h"  // sdpa_status_t codes (shared with the GPU library)
 
@@ -338,6 +339,22 @@ Problem make_problem(int dtype, int B, int S_q, int S_kv, int D_qk, int D_v, flo
 }  // namespace
 
 extern "C" {
+
+const char* sdpa_cpu_status_string(int status) { return sdpa::status_message(status); }
+
+int sdpa_cpu_check_fwd(int q_rank, const int64_t* q_shape, int k_rank, const int64_t* k_shape, int v_rank,
+                       const int64_t* v_shape, int seed_rank, int offset_rank, int causal_mask) {
+    return sdpa::check_fwd_shapes(q_rank, q_shape, k_rank, k_shape, v_rank, v_shape, seed_rank, offset_rank,
+                                  causal_mask);
+}
+
+int sdpa_cpu_check_bwd(int q_rank, const int64_t* q_shape, int k_rank, const int64_t* k_shape, int v_rank,
+                       const int64_t* v_shape, int o_rank, const int64_t* o_shape, int stats_rank,
+                       const int64_t* stats_shape, int do_rank, const int64_t* do_shape, int seed_rank,
+                       int offset_rank, int causal_mask) {
+    return sdpa::check_bwd_shapes(q_rank, q_shape, k_rank, k_shape, v_rank, v_shape, o_rank, o_shape, stats_rank,
+                                  stats_shape, do_rank, do_shape, seed_rank, offset_rank, causal_mask);
+}
 
 int sdpa_cpu_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* stats,
                  int B, int S_q, int S_kv, int D_qk, int D_v, float scale, float dropout,
