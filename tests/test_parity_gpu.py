@@ -195,18 +195,20 @@ def test_fp16_large_outputs_few_keys(pkg, O, D, p):
     rounds, sdpa_cpu.cc:308), so the error holds the kernel's own output
     rounding (at most half an ulp) plus its arithmetic error.
 
-    Rows 0-63 (at most 64 visible keys; the forward feeds P~ to the PV
-    product as two fp16 parts there):
-      |o - o_ref| <= ulp(o_ref) / 2 + 1e-5     (o is o_ref correctly rounded)
-      |o - o_ref| <= 2e-3 where |o_ref| < 8    (north_star's o gate; from 8 on
-                                                 half an ulp alone exceeds it)
-    Rows 64 on (fp16 P~ in the PV product): the error is bounded by the
-    rounding of each P_j to fp16, |dP_j| <= 2^-11 P_j, i.e.
-      |o - o_ref| <= ulp(o_ref) / 2 + 2^-11 sum_j P~_j |v_j| / l + 1e-4
+    Where a few keys carry a row's mass, the kernels feed P~ to the PV
+    product as two fp16 parts, hi + lo (every 32- or 64-key tile in which one
+    key holds more than 1/8 of the mass seen before it).  Asserted:
+      rows 0-63 (at most 64 visible keys, every tile split):
+        |o - o_ref| <= ulp(o_ref) / 2 + 1e-5        (o is o_ref correctly rounded)
+      every row, wherever |o_ref| < 4 (half an ulp <= 9.8e-4):
+        |o - o_ref| <= 2e-3                          (north_star's o gate)
+      rows 0-63 wherever |o_ref| < 8 (from 8 on half an ulp alone exceeds it):
+        |o - o_ref| <= 2e-3
+    and, for rows 64 on, the bound of an unsplit tile's fp16 P~ (each P_j
+    rounded, |dP_j| <= 2^-11 P_j):
+        |o - o_ref| <= ulp(o_ref) / 2 + 2^-11 sum_j P~_j |v_j| / l + 1e-4
     with P_j / l = exp(scale q.k_j - stats) from the oracle's statistics (the
-    1e-4 covers P~ below fp16's normal range).  With V ~ N(0, 36) that bound
-    reaches ~1.2e-3 in peaked rows, so the 2e-3 gate is not asserted there;
-    the BASELINE configurations (V ~ N(0, 1)) meet it in every row."""
+    1e-4 covers P~ below fp16's normal range)."""
     c = Cfg(f"margin_d{D}_p{p}", "f16", 4, 256, 256, D, D, True, p, D ** -0.5, 7, 0)
     q, k, v, _ = make_inputs(c)
     v = (v.astype(np.float32) * 6).astype(np.float16)
@@ -233,12 +235,15 @@ def test_fp16_large_outputs_few_keys(pkg, O, D, p):
     p16 = 2.0 ** -11 * np.einsum("bij,bjd->bid", pl, np.abs(v.astype(np.float64)))
     excess_few = float((err[:, few] - half_ulp[:, few]).max())
     gate_few = err[:, few][np.abs(o_ref[:, few]) < 8].max()
+    gate_all = err[np.abs(o_ref) < 4].max()
     excess_rest = float((err[:, 64:] - half_ulp[:, 64:] - p16[:, 64:]).max())
     print(f"[errs] {c.name}: rows<64 max excess over half ulp={excess_few:.2e} max|o-o_ref|(|o|<8)="
-          f"{gate_few:.3e}; rows>=64 max|o-o_ref|={err[:, 64:].max():.3e} excess over the fp16-P bound="
-          f"{excess_rest:.2e}; stats={maxabs(_np(s), s_ref):.2e}", flush=True)
+          f"{gate_few:.3e}; all rows max|o-o_ref|(|o|<4)={gate_all:.3e}; rows>=64 max|o-o_ref|="
+          f"{err[:, 64:].max():.3e} excess over the fp16-P bound={excess_rest:.2e}; "
+          f"stats={maxabs(_np(s), s_ref):.2e}", flush=True)
     assert excess_few <= 1e-5
     assert gate_few <= 2e-3
+    assert gate_all <= 2e-3
     assert excess_rest <= 1e-4
     assert maxabs(_np(s), s_ref) <= TOL["f16"]["stats"]
 

@@ -59,6 +59,21 @@ __device__ __forceinline__ floatx16 mfma_f32(float a, float b, const floatx16& c
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// v_log_f32: log2, -inf at 0
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Hi/lo split of P~ in the PV product.  A key sub-tile's P~ enters the fp16
+// MFMA as one fp16 part, relative rounding 2^-11 per element; where a few
+// keys carry a row's mass that moves o by up to 2^-11 |v|, which for |v| of
+// a few units is more than half an fp16 ulp of o.  The kernels then add the
+// remainder P~ - fp16(P~) as a second fp16 part (P~ to ~2^-22).  A sub-tile
+// is split when some row of the wave has a score above the row's running
+// log2-sum-exp (m + log2 l over the keys before it, refreshed once per key
+// block) + kSplitLog2, i.e. one key of the sub-tile would hold more than 2^-3
+// of the mass seen so far.  The log-sum-exp does not move when the running
+// maximum is rescaled, and one refreshed less often is smaller, so the test
+// only errs towards splitting.
+constexpr float kSplitLog2 = -3.0f;
 
 // Value of lane l^32 combined with the own value: permlane32_swap exchanges the
 // upper half of the first operand with the lower half of the second, so the

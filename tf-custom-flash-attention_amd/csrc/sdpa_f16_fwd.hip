@@ -145,11 +145,10 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
     // -inf by the caller): per-lane lazy maximum m_use (moves only when the
     // block maximum exceeds the running one by more than 2^kTauF), alpha =
     // exp2(m_run - m_use), P = exp2(s sl2 - m_use), the undropped sum and the
-    // dropped, fp16-packed B operands of the PV product.
-    // SPLIT: also the fp16 remainders pl = P~ - fp16(P~), so that the PV
-    // product sees P~ to ~2^-22 (rows averaging only a few keys, below).
-    auto softmax_sub = [&]<bool SPLIT>(const floatx16& sc, int t, uint64_t st_blk, float& m_use, float& alpha,
-                                       float& lsum, half8& pb0, half8& pb1, half8& pl0, half8& pl1) {
+    // dropped, fp16-packed B operands of the PV product; also the row maximum
+    // mxo (log2 units) and the dropped P~ in fp32 (pf, for the hi/lo split).
+    auto softmax_sub = [&](const floatx16& sc, int t, uint64_t st_blk, float& m_use, float& alpha, float& lsum,
+                           float& mxo, half8& pb0, half8& pb1, float (&pf)[16]) {
         // a chain of v_max3 (one per two scores): the opaque steps keep the
         // compiler from re-associating it into a tree of v_max and v_max3,
         // which costs ~1.4 instructions per two scores
@@ -161,10 +160,11 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
         }
         mx = fmaxf(mx, sc[15]);
         mx = xhalf_max(mx) * sl2;
+        mxo = mx;
         m_use = (mx > m_run + kTauF) ? fmaxf(m_run, mx) : m_run;
         alpha = fast_exp2(m_run - m_use);
         const float nm = -m_use;
-        uint32_t w[8], wl[8];
+        uint32_t w[8];
         float lq[4];
         // Hash states walk the lane's keys 32 t + 8 g + e as a chain of adds
         // (opaque to the compiler, which would otherwise fold them into 32
@@ -191,19 +191,26 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
             }
             w[r >> 1] = pack_h2(pq[0], pq[1]);
             w[(r >> 1) + 1] = pack_h2(pq[2], pq[3]);
-            if constexpr (SPLIT) {
-                const half2v h0 = __builtin_bit_cast(half2v, w[r >> 1]);
-                const half2v h1 = __builtin_bit_cast(half2v, w[(r >> 1) + 1]);
-                wl[r >> 1] = pack_h2(pq[0] - (float)h0[0], pq[1] - (float)h0[1]);
-                wl[(r >> 1) + 1] = pack_h2(pq[2] - (float)h1[0], pq[3] - (float)h1[1]);
-            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pf[r + e] = pq[e];
         }
         lsum = (lq[0] + lq[1]) + (lq[2] + lq[3]);
         pb0 = half8_of(w[0], w[1], w[2], w[3]);
         pb1 = half8_of(w[4], w[5], w[6], w[7]);
-        if constexpr (SPLIT) {
-            pl0 = half8_of(wl[0], wl[1], wl[2], wl[3]);
-            pl1 = half8_of(wl[4], wl[5], wl[6], wl[7]);
+    };
+    // The lo part of a split sub-tile: O^T += V^T (P~ - fp16(P~))^T.
+    auto lo_pv = [&](const half8 (&av)[2][NDT], const half8& pb0, const half8& pb1, const float (&pf)[16]) {
+        uint32_t wl[8];
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) {
+            wl[i >> 1] = pack_h2(pf[i] - (float)pb0[i], pf[i + 1] - (float)pb0[i + 1]);
+            wl[4 + (i >> 1)] = pack_h2(pf[8 + i] - (float)pb1[i], pf[9 + i] - (float)pb1[i + 1]);
+        }
+        const half8 l0 = half8_of(wl[0], wl[1], wl[2], wl[3]), l1 = half8_of(wl[4], wl[5], wl[6], wl[7]);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            oacc[dt] = mfma_f16(av[0][dt], l0, oacc[dt]);
+            oacc[dt] = mfma_f16(av[1][dt], l1, oacc[dt]);
         }
     };
     // Mask of sub-tile t: keys past S_kv and, causal, keys after the query.
@@ -239,14 +246,13 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
     // PV(0) accumulation, so it is applied after R3.
     // mid(k) marks the end of region k (the copy points of the step).
     //
-    // SPLIT (the first key block of a masked step: every row of the wave sees
-    // at most 64 keys): P~ enters the PV product as two fp16 parts, hi + lo.
-    // Over many keys the fp16 rounding of P~ (relative 2^-12) averages out;
-    // over one or two keys it would move o by up to 2^-12 |v|, more than
-    // half an fp16 ulp of o.
-    auto fwd_step = [&]<bool PART, bool SPLIT>(int kv0, uint32_t so, auto&& mid) {
+    // A sub-tile whose largest score passes the row's split threshold thr
+    // (the running log2-sum-exp before this step + kSplitLog2; -inf before
+    // any key) also adds its lo part (lo_pv, a rare wave-uniform branch).
+    auto fwd_step = [&]<bool PART>(int kv0, uint32_t so, auto&& mid) {
         const bool part0 = PART && (kv0 + 32 > S_kv || (CAUSAL && kv0 + 31 > qw0));
         const bool part1 = PART && (kv0 + 64 > S_kv || (CAUSAL && kv0 + 63 > qw0));
+        const float thr = m_run + fast_log2(xhalf_sum(l_run)) + kSplitLog2;
         // Read addresses of this step, formed here (opaque lane terms keep the
         // compiler from hoisting twelve of them into registers for the loop).
         uint32_t kl = rkl, vl = tvl;
@@ -277,20 +283,17 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
             for (int dt = 0; dt < NDT; ++dt)
                 av0[j][dt] = ld_tr8(tv[dt] + 16 * LV * 16 * j, tv[dt] + 16 * LV * (16 * j + 8));
         if (part0) mask_sub(s0, kv0, 0);
-        float mu0, al0, ls0;
-        half8 p00, p01, l00, l01;
-        softmax_sub.template operator()<SPLIT>(s0, 0, st_blk, mu0, al0, ls0, p00, p01, l00, l01);
+        float mu0, al0, ls0, mx0, pf0[16];
+        half8 p00, p01;
+        softmax_sub(s0, 0, st_blk, mu0, al0, ls0, mx0, p00, p01, pf0);
         commit_sub(mu0, al0, ls0);
         mid(2);
         // R3
+        if (wave_any(mx0 > thr)) lo_pv(av0, p00, p01, pf0);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             oacc[dt] = mfma_f16(av0[0][dt], p00, oacc[dt]);
             oacc[dt] = mfma_f16(av0[1][dt], p01, oacc[dt]);
-            if constexpr (SPLIT) {
-                oacc[dt] = mfma_f16(av0[0][dt], l00, oacc[dt]);
-                oacc[dt] = mfma_f16(av0[1][dt], l01, oacc[dt]);
-            }
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
@@ -298,20 +301,17 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
             for (int dt = 0; dt < NDT; ++dt)
                 av1[j][dt] = ld_tr8(tv[dt] + 16 * LV * (32 + 16 * j), tv[dt] + 16 * LV * (40 + 16 * j));
         if (part1) mask_sub(s1, kv0, 1);
-        float mu1, al1, ls1;
-        half8 p10, p11, l10, l11;
-        softmax_sub.template operator()<SPLIT>(s1, 1, st_blk, mu1, al1, ls1, p10, p11, l10, l11);
+        float mu1, al1, ls1, mx1, pf1[16];
+        half8 p10, p11;
+        softmax_sub(s1, 1, st_blk, mu1, al1, ls1, mx1, p10, p11, pf1);
         commit_sub(mu1, al1, ls1);
         mid(3);
         // R4
+        if (wave_any(mx1 > thr)) lo_pv(av1, p10, p11, pf1);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             oacc[dt] = mfma_f16(av1[0][dt], p10, oacc[dt]);
             oacc[dt] = mfma_f16(av1[1][dt], p11, oacc[dt]);
-            if constexpr (SPLIT) {
-                oacc[dt] = mfma_f16(av1[0][dt], l10, oacc[dt]);
-                oacc[dt] = mfma_f16(av1[1][dt], l11, oacc[dt]);
-            }
         }
     };
 
@@ -337,8 +337,7 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
             if (cp && wave == k) issue(step + NSTAGE - 1);
         };
         if (!PART || (live && !(CAUSAL && kv0 > qw0 + 31))) {  // else: no visible key in this step
-            if (PART && step == 0) fwd_step.template operator()<PART, true>(kv0, so, mid);
-            else fwd_step.template operator()<PART, false>(kv0, so, mid);
+            fwd_step.template operator()<PART>(kv0, so, mid);
         }
         else if (cp && wave != 0)
             issue(step + NSTAGE - 1);

@@ -56,10 +56,10 @@ struct FwdF16Cfg {
     static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE * sizeof(half_t);
 };
 
-// Two waves per SIMD throughout: with the split-variant loop beside the main
-// one, <128,128> (aligned rows, no dropout) keeps 20 bytes per lane in
-// scratch and <64,128> (generic row loads, no dropout) 8; one wave per SIMD,
-// spill-free, measured 5-6.5% slower at D = 124 and 60 / 124.
+// Two waves per SIMD throughout: with the split pass in the block loop,
+// <128,128> with dropout keeps 32 (aligned rows) and 88 (generic row loads)
+// bytes per lane in scratch, every other instantiation none; one wave per
+// SIMD, spill-free, measured 5-6.5% slower at D = 124 and 60 / 124.
 template <int DQK, int DV, bool VEC, bool DROP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_fwd_f16_kernel(const FwdParams p) {
@@ -121,11 +121,83 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
     }
     __syncthreads();
 
-    // One key block.  SPLIT (rows that see at most BN keys in all): P~
-    // enters the PV product as two fp16 parts, hi + lo.  Over one or two keys
-    // the fp16 rounding of P~ (2^-12 relative) would move o by more than half
-    // an fp16 ulp; over many keys it averages out.
-    auto block = [&]<bool SPLIT>(int blk) {
+    // S^T = K Q^T of one key block, log2-scaled, masked keys -inf.
+    auto scores = [&](floatx16 (&sacc)[BN / 32], const half_t* Ks, int kv0) {
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t) sacc[t] = floatx16{};
+#pragma unroll
+        for (int ks = 0; ks < DQK / 16; ++ks) {
+#pragma unroll
+            for (int t = 0; t < BN / 32; ++t) {
+                const half8 a = *reinterpret_cast<const half8*>(Ks + swz_off<LK>(32 * t + l32, 16 * ks + 8 * hh));
+                sacc[t] = mfma_f16(a, qreg[ks], sacc[t]);
+            }
+        }
+        const bool need_mask = (kv0 + BN > S_kv) || (causal && kv0 + BN - 1 > qw0);
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float x = sacc[t][r] * sl2;
+                if (need_mask) {
+                    const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    if (key >= S_kv || (causal && key > my_q)) x = -INFINITY;
+                }
+                sacc[t][r] = x;
+            }
+        }
+    };
+    // P~ = exp2(s - m_run) with dropout, as fp16 B operands of the PV product:
+    // LO = false the values (pb; the undropped sum goes into l_run), LO = true
+    // their remainders P~ - fp16(P~) (the lo part of the hi/lo split).
+    auto probs = [&]<bool LO>(const floatx16 (&sacc)[BN / 32], int kv0, half8 (&pb)[BN / 16]) {
+        const uint64_t st_blk = DROP ? st_base + (uint64_t)kv0 * kLcgMul : 0;
+        float lsum = 0.f;
+#pragma unroll
+        for (int t = 0; t < BN / 32; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                float p0 = fast_exp2(sacc[t][r] - m_run);
+                float p1 = fast_exp2(sacc[t][r + 1] - m_run);
+                lsum += p0;
+                lsum += p1;
+                if constexpr (DROP) {
+                    const uint64_t o0 = (uint64_t)(32 * t + 8 * (r >> 2) + (r & 3)) * kLcgMul;
+                    const uint64_t o1 = (uint64_t)(32 * t + 8 * ((r + 1) >> 2) + ((r + 1) & 3)) * kLcgMul;
+                    p0 = lcg_keep(st_blk + o0, thr) ? p0 : 0.f;
+                    p1 = lcg_keep(st_blk + o1, thr) ? p1 : 0.f;
+                }
+                half2v hp = cvt_pk(p0, p1);
+                if constexpr (LO) hp = cvt_pk(p0 - (float)hp[0], p1 - (float)hp[1]);
+                const int s = 2 * t + (r >> 3), i = r & 7;
+                pb[s][i] = hp[0];
+                pb[s][i + 1] = hp[1];
+            }
+        }
+        if constexpr (!LO) l_run += lsum;
+    };
+    // O^T += V^T P~^T
+    auto pv = [&](const half_t* Vs, const half8 (&pb)[BN / 16]) {
+#pragma unroll
+        for (int s = 0; s < BN / 16; ++s) {
+#pragma unroll
+            for (int dt = 0; dt < DV / 32; ++dt) {
+                const half4 a0 = lds_read_tr(Vs + swz_off<LV>(16 * s + tr_row, 32 * dt + tr_col));
+                const half4 a1 = lds_read_tr(Vs + swz_off<LV>(16 * s + 8 + tr_row, 32 * dt + tr_col));
+                const half8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+                oacc[dt] = mfma_f16(a, pb[s], oacc[dt]);
+            }
+        }
+    };
+
+    // One key block.  The hi/lo split of P~ (sdpa_device.h, kSplitLog2) is
+    // decided per block: when some row's block maximum passes its running
+    // log2-sum-exp (before the block) + kSplitLog2, the block's lo part is
+    // added after the next block's tiles have left their staging registers
+    // for LDS: S and P~ are formed again from the block's LDS tiles (same
+    // instructions on the same operands: the same values), so that nothing
+    // of the first pass stays live across it.
+    auto block = [&](int blk) {
         const int kv0 = blk * BN;
         const half_t* Ks = lds + (blk & 1) * Cfg::STAGE;
         const half_t* Vs = Ks + Cfg::KT;
@@ -135,36 +207,18 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
             vst.load(Vb, kv0 + BN, S_kv - kv0 - BN, D_v, D_v, tid);
         }
 
+        bool split = false;
         if (wave_live && (!causal || kv0 <= wave_last_q)) {
-            // ---- S^T = K Q^T --------------------------------------------
+            const float split_thr = m_run + fast_log2(xhalf_sum(l_run)) + kSplitLog2;
             floatx16 sacc[BN / 32];
-#pragma unroll
-            for (int t = 0; t < BN / 32; ++t) sacc[t] = floatx16{};
-#pragma unroll
-            for (int ks = 0; ks < DQK / 16; ++ks) {
-#pragma unroll
-                for (int t = 0; t < BN / 32; ++t) {
-                    const half8 a = *reinterpret_cast<const half8*>(Ks + swz_off<LK>(32 * t + l32, 16 * ks + 8 * hh));
-                    sacc[t] = mfma_f16(a, qreg[ks], sacc[t]);
-                }
-            }
-            // ---- scale, mask, block max ----------------------------------
-            const bool need_mask = (kv0 + BN > S_kv) || (causal && kv0 + BN - 1 > qw0);
+            scores(sacc, Ks, kv0);
             float mx = -INFINITY;
 #pragma unroll
-            for (int t = 0; t < BN / 32; ++t) {
+            for (int t = 0; t < BN / 32; ++t)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float x = sacc[t][r] * sl2;
-                    if (need_mask) {
-                        const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * hh + (r & 3);
-                        if (key >= S_kv || (causal && key > my_q)) x = -INFINITY;
-                    }
-                    sacc[t][r] = x;
-                    mx = fmaxf(mx, x);
-                }
-            }
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[t][r]);
             mx = xhalf_max(mx);
+            split = wave_any(mx > split_thr);
             const float m_new = fmaxf(m_run, mx);
             if (wave_any(m_new > m_run + kTau)) {
                 const float alpha = fast_exp2(m_run - m_new);
@@ -175,48 +229,9 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
                     for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
                 m_run = m_new;
             }
-            // ---- probabilities, dropout, fp16 B operands ------------------
-            const uint64_t st_blk = DROP ? st_base + (uint64_t)kv0 * kLcgMul : 0;
-            float lsum = 0.f;
-            half8 pb[BN / 16], pl[BN / 16];
-#pragma unroll
-            for (int t = 0; t < BN / 32; ++t) {
-#pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    float p0 = fast_exp2(sacc[t][r] - m_run);
-                    float p1 = fast_exp2(sacc[t][r + 1] - m_run);
-                    lsum += p0;
-                    lsum += p1;
-                    if constexpr (DROP) {
-                        const uint64_t o0 = (uint64_t)(32 * t + 8 * (r >> 2) + (r & 3)) * kLcgMul;
-                        const uint64_t o1 = (uint64_t)(32 * t + 8 * ((r + 1) >> 2) + ((r + 1) & 3)) * kLcgMul;
-                        p0 = lcg_keep(st_blk + o0, thr) ? p0 : 0.f;
-                        p1 = lcg_keep(st_blk + o1, thr) ? p1 : 0.f;
-                    }
-                    const half2v hp = cvt_pk(p0, p1);
-                    const int s = 2 * t + (r >> 3), i = r & 7;
-                    pb[s][i] = hp[0];
-                    pb[s][i + 1] = hp[1];
-                    if constexpr (SPLIT) {
-                        const half2v hl = cvt_pk(p0 - (float)hp[0], p1 - (float)hp[1]);
-                        pl[s][i] = hl[0];
-                        pl[s][i + 1] = hl[1];
-                    }
-                }
-            }
-            l_run += lsum;
-            // ---- O^T += V^T P~^T ------------------------------------------
-#pragma unroll
-            for (int s = 0; s < BN / 16; ++s) {
-#pragma unroll
-                for (int dt = 0; dt < DV / 32; ++dt) {
-                    const half4 a0 = lds_read_tr(Vs + swz_off<LV>(16 * s + tr_row, 32 * dt + tr_col));
-                    const half4 a1 = lds_read_tr(Vs + swz_off<LV>(16 * s + 8 + tr_row, 32 * dt + tr_col));
-                    const half8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
-                    oacc[dt] = mfma_f16(a, pb[s], oacc[dt]);
-                    if constexpr (SPLIT) oacc[dt] = mfma_f16(a, pl[s], oacc[dt]);
-                }
-            }
+            half8 pb[BN / 16];
+            probs.template operator()<false>(sacc, kv0, pb);
+            pv(Vs, pb);
         }
 
         if (has_next) {
@@ -224,17 +239,20 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
             kst.store_swz(Kn, tid);
             vst.store_swz(Kn + Cfg::KT, tid);
         }
+        if (split) {
+            // opaque copies of the tile offset and key index: nothing here
+            // is merged with the first pass
+            int z = 0, kz = kv0;
+            asm volatile("" : "+s"(z), "+s"(kz));
+            floatx16 sacc[BN / 32];
+            scores(sacc, Ks + z, kz);
+            half8 pl[BN / 16];
+            probs.template operator()<true>(sacc, kz, pl);
+            pv(Vs + z, pl);
+        }
         __syncthreads();
     };
-    // Only waves whose rows all lie below key BN (or S_kv < BN) take the
-    // split, and for them the first block is the only visible one: such a
-    // wave runs the split variant in a loop of its own (one loop choosing per
-    // block merged the accumulators of the two variants with register copies).
-    if (S_kv < BN || (causal && qw0 < BN - 1)) {
-        for (int blk = 0; blk < nblk; ++blk) block.template operator()<true>(blk);
-    } else {
-        for (int blk = 0; blk < nblk; ++blk) block.template operator()<false>(blk);
-    }
+    for (int blk = 0; blk < nblk; ++blk) block(blk);
 
     // ---- epilogue: stats and O = acc / l ----------------------------------
     const float l_tot = xhalf_sum(l_run);
