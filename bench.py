@@ -5,7 +5,12 @@ Workload (the config the metric is quoted on):
 fp16, batch = B*H = 128, S_q = S_kv = 4096, D_qk = D_v = 128, causal,
 dropout 0.1 (seed 7, offset 0), scale 1/sqrt(128), q/k/v/dO ~ N(0,1)
 (synthetic, seeded).  A "step" is one forward (1 kernel) plus one backward
-(dQ kernel, then dK/dV kernel) over that batch, inputs resident in HBM.
+over that batch, inputs resident in HBM.  The backward takes its dS path
+(fp16 with a feature size over 64, given the workspace of
+sdpa_hip_bwd_workspace_bytes_ds): the row kernel (stats2, delta), the dK/dV
+kernel that also stores dS, and dQ as one product with the stored dS;
+--bwd-path recompute times the path that forms dS in both kernels (dQ
+kernel, then dK/dV kernel) instead.
 
 FLOPs follow the FlashAttention convention (causal x1/2, dropout RNG not
 counted):  fwd = 2*B*S_q*S_kv*(D_qk+D_v)/2,  bwd = 2*B*S_q*S_kv*(3*D_qk+2*D_v)/2.
@@ -129,6 +134,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU baseline threads (0: auto)")
     ap.add_argument("--cold-steps", type=int, default=5,
                     help="extra steps timed with the caches flushed before every kernel (0: skip)")
+    ap.add_argument("--bwd-path", default="ds", choices=["ds", "recompute"],
+                    help="backward path: ds (where the shape allows) or recompute")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
@@ -167,7 +174,10 @@ def main():
     o = torch.empty((B, S_q, D_v), dtype=tdt, device=dev)
     st = torch.empty((B, S_q), dtype=torch.float32, device=dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws_bytes = int(L.sdpa_hip_bwd_workspace_bytes(B, S_q))
+    rows_bytes = int(L.sdpa_hip_bwd_workspace_bytes(B, S_q))
+    ds_bytes = int(L.sdpa_hip_bwd_workspace_bytes_ds(dcode, B, S_q, S_kv, D_qk, D_v, int(causal)))
+    use_ds = args.bwd_path == "ds" and ds_bytes > rows_bytes
+    ws_bytes = ds_bytes if use_ds else rows_bytes
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
     h = stream.cuda_stream  # every launch below goes to this stream
@@ -193,7 +203,19 @@ def main():
                                   ws_bytes, B, S_q, S_kv, D_qk, D_v, scale, p, int(causal), seed,
                                   off, h))
 
-    phases = [("sdpa_fwd", fwd), ("sdpa_bwd_dq", bwd_dq), ("sdpa_bwd_dkdv", bwd_dkdv)]
+    def ds_phase(i):
+        def run():
+            check(L.sdpa_hip_bwd_ds_phase(i, dcode, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                          st.data_ptr(), d_o.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                                          dv.data_ptr(), ws.data_ptr(), ws_bytes, B, S_q, S_kv, D_qk, D_v,
+                                          scale, p, int(causal), seed, off, h))
+        return run
+
+    if use_ds:
+        phases = [("sdpa_fwd", fwd), ("sdpa_bwd_rows", ds_phase(0)), ("sdpa_bwd_dkdv", ds_phase(1)),
+                  ("sdpa_bwd_dq", ds_phase(2))]
+    else:
+        phases = [("sdpa_fwd", fwd), ("sdpa_bwd_dq", bwd_dq), ("sdpa_bwd_dkdv", bwd_dkdv)]
     for _ in range(args.warmup):
         for _, fn in phases:
             fn()
@@ -245,18 +267,20 @@ def main():
 
     f_fwd, f_dq, f_dkdv = flops(cfg)
     f_bwd = f_dq + f_dkdv
-    fwd_ms, bwd_ms = med["sdpa_fwd"], med["sdpa_bwd_dq"] + med["sdpa_bwd_dkdv"]
+    fwd_ms, bwd_ms = med["sdpa_fwd"], sum(t for n_, t in med.items() if n_ != "sdpa_fwd")
     peak = PEAK_F16_TFLOPS if dt == "f16" else PEAK_F32_TFLOPS
     value = (f_fwd + f_bwd) / (step_med * 1e-3) / 1e12
-    kflops = {"sdpa_fwd": f_fwd, "sdpa_bwd_dq": f_dq, "sdpa_bwd_dkdv": f_dkdv}
+    kflops = {"sdpa_fwd": f_fwd, "sdpa_bwd_dq": f_dq, "sdpa_bwd_dkdv": f_dkdv, "sdpa_bwd_rows": 0.0}
     dom = max(per, key=per.get)
     achieved = kflops[dom] / (per[dom] * 1e-3) / 1e12
     # fp16 shapes with D % 8 == 0 run the DMA-fed kernels (sdpa_f16_fwd/dq/dkdv.hip)
     sfx = "f16_dma" if (dt == "f16" and D_qk % 8 == 0 and D_v % 8 == 0) else dt
     # (dK/dV of a feature width above 64 runs the split-role variant)
     kv_sfx = "f16_split" if (sfx == "f16_dma" and max(D_qk, D_v) > 64) else sfx
-    kernel_symbol = {"sdpa_fwd": "sdpa_fwd_%s_kernel" % sfx, "sdpa_bwd_dq": "sdpa_bwd_dq_%s_kernel" % sfx,
-                     "sdpa_bwd_dkdv": "sdpa_bwd_dkdv_%s_kernel" % kv_sfx}[dom]
+    dq_sym = "sdpa_bwd_dq_ds_f16_kernel" if use_ds else "sdpa_bwd_dq_%s_kernel" % sfx
+    kernel_symbol = {"sdpa_fwd": "sdpa_fwd_%s_kernel" % sfx, "sdpa_bwd_dq": dq_sym,
+                     "sdpa_bwd_dkdv": "sdpa_bwd_dkdv_%s_kernel" % kv_sfx,
+                     "sdpa_bwd_rows": "sdpa_bwd_rows_f16_kernel"}[dom]
 
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * (1 << 20)
@@ -294,6 +318,8 @@ def main():
         "bwd_tflops": round(f_bwd / (bwd_ms * 1e-3) / 1e12, 3),
         "fwd_pct_peak": round(100.0 * f_fwd / (fwd_ms * 1e-3) / 1e12 / peak, 2),
         "bwd_pct_peak": round(100.0 * f_bwd / (bwd_ms * 1e-3) / 1e12 / peak, 2),
+        "bwd_path": "ds" if use_ds else "recompute",
+        "workspace_bytes": ws_bytes,
         "kernel_ms": {k_: round(v_, 4) for k_, v_ in per.items()},
         "kernel_ms_median": {k_: round(v_, 4) for k_, v_ in med.items()},
         "kernel_ms_cache_cold": cold,

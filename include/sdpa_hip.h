@@ -69,7 +69,8 @@ typedef enum {
     SDPA_ERR_DROPOUT_RANGE = 21,
     SDPA_ERR_WORKSPACE = 22,
     SDPA_ERR_HIP = 23,
-    SDPA_ERR_SCRATCH_LIMIT = 24
+    SDPA_ERR_SCRATCH_LIMIT = 24,
+    SDPA_ERR_DS_PATH = 25
 } sdpa_status_t;
 
 /* Message for a status code (static storage, never NULL). */
@@ -135,6 +136,33 @@ int sdpa_hip_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, co
                       size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
                       float scale, float dropout, int causal_mask, uint64_t seed,
                       uint64_t offset, hipStream_t stream);
+
+/* ---- backward, dS path --------------------------------------------------
+ * No counterpart in the reference (an MI355X choice of how its two backward
+ * kernels divide the work).  For float16 with a feature size over 64, the
+ * dK/dV kernel can store the dS it forms (fp16, every visited score: about
+ * B * S_q * S_kv bytes under the causal mask, twice that without) and dQ is
+ * then one product with it, instead of a kernel that forms S, P, dP and dS
+ * again.  sdpa_hip_bwd takes this path whenever the shape qualifies, the
+ * tensors are 16-byte aligned and workspace_bytes is at least
+ * sdpa_hip_bwd_workspace_bytes_ds(...); with a smaller workspace (at least
+ * sdpa_hip_bwd_workspace_bytes(B, S_q)) it takes the other one.  For shapes
+ * that do not qualify the function returns sdpa_hip_bwd_workspace_bytes. */
+size_t sdpa_hip_bwd_workspace_bytes_ds(int dtype, int B, int S_q, int S_kv, int D_qk, int D_v,
+                                       int causal_mask);
+
+/* The three launches of the dS path as separate calls (same arguments as
+ * sdpa_hip_bwd; each phase reads what the previous one left in the workspace,
+ * in stream order):
+ *   phase 0 -- the per-row values (stats * log2(e), delta) into the workspace;
+ *   phase 1 -- dK, dV and the stored dS;
+ *   phase 2 -- dQ from the stored dS.
+ * Returns SDPA_ERR_DS_PATH where sdpa_hip_bwd would not take the dS path.  */
+int sdpa_hip_bwd_ds_phase(int phase, int dtype, const void* q, const void* k, const void* v,
+                          const void* o, const float* stats, const void* d_o, void* dq, void* dk,
+                          void* dv, void* workspace, size_t workspace_bytes, int B, int S_q,
+                          int S_kv, int D_qk, int D_v, float scale, float dropout, int causal_mask,
+                          uint64_t seed, uint64_t offset, hipStream_t stream);
 
 /* ---- backward that allocates nothing ---------------------------------------
  * No counterpart in the reference.  For callers that cannot allocate device

@@ -60,8 +60,8 @@ REF_MESSAGES = {
 def test_status_strings(pkg):
     for code, msg in REF_MESSAGES.items():
         assert pkg.status_string(code) == msg
-    for code in range(0, 25):
-        assert pkg.status_string(code)
+    for code in range(0, 26):
+        assert pkg.status_string(code) != "unknown sdpa status"
 
 
 class Shape:
@@ -157,6 +157,59 @@ def test_launch_entry_points_reject_before_device_work(pkg):
     # two fp32 rows per query row: stats * log2(e) and delta
     assert L.sdpa_hip_bwd_workspace_bytes(128, 4096) == 2 * 128 * 4096 * 4
     assert L.sdpa_hip_bwd_workspace_bytes(0, 4096) == 0
+
+
+def _ds_chunks(S_q, S_kv, causal):
+    """Query blocks (64 rows) the split dK/dV kernel visits, summed over its
+    key tiles (128 keys): the dS chunks of one batch row, counted the way the
+    kernel walks them (q_begin, nsteps of sdpa_f16_dkdv_split.hip)."""
+    n = 0
+    for kt in range((S_kv + 127) // 128):
+        q_begin = (min(128 * kt, S_q) // 64) * 64 if causal else 0
+        n += (S_q - q_begin + 63) // 64
+    return n
+
+
+def test_ds_workspace_bytes(pkg):
+    """sdpa_hip_bwd_workspace_bytes_ds = the per-row workspace + 16 KB per
+    visited (key tile, query block) per batch row, for float16 with a feature
+    size over 64; the per-row size for every other shape."""
+    L = pkg.library()
+    for B, S_q, S_kv, D_qk, D_v, causal in [(128, 4096, 4096, 128, 128, 1), (3, 333, 333, 128, 128, 1),
+                                             (2, 130, 300, 128, 64, 0), (2, 300, 100, 64, 128, 0),
+                                             (1, 1, 1, 128, 128, 1), (1, 31, 1000, 80, 80, 0),
+                                             (5, 1000, 1000, 96, 96, 1), (2, 64, 64, 128, 128, 1)]:
+        rows = L.sdpa_hip_bwd_workspace_bytes(B, S_q)
+        want = rows + B * _ds_chunks(S_q, S_kv, causal) * 16384
+        assert L.sdpa_hip_bwd_workspace_bytes_ds(1, B, S_q, S_kv, D_qk, D_v, causal) == want
+        # fp32, or both sides <= 64: the per-row workspace only
+        assert L.sdpa_hip_bwd_workspace_bytes_ds(0, B, S_q, S_kv, D_qk, D_v, causal) == rows
+        assert L.sdpa_hip_bwd_workspace_bytes_ds(1, B, S_q, S_kv, 64, 64, causal) == rows
+    # c4: 1056 chunks per batch row under the causal mask (half of 32 x 64, plus the diagonal)
+    assert _ds_chunks(4096, 4096, True) == 1056
+    assert L.sdpa_hip_bwd_workspace_bytes_ds(1, 0, 4096, 4096, 128, 128, 1) == 0
+    assert L.sdpa_hip_bwd_workspace_bytes_ds(1, 2, 64, 0, 128, 128, 0) == L.sdpa_hip_bwd_workspace_bytes(2, 64)
+
+
+def test_ds_phase_rejects_before_device_work(pkg):
+    """sdpa_hip_bwd_ds_phase returns SDPA_ERR_DS_PATH where sdpa_hip_bwd would
+    not take the dS path; the stand-in addresses (16-byte aligned, never
+    dereferenced on the host) are refused before any launch."""
+    L = pkg.library()
+    fake = 4096
+    big = 1 << 40
+
+    def phase(ph, dtype, D_qk=128, D_v=128, ws=big, B=2):
+        return L.sdpa_hip_bwd_ds_phase(ph, dtype, *([fake] * 10), ws, B, 64, 64, D_qk, D_v, 1.0, 0.0, 1, 0, 0,
+                                       None)
+    assert phase(0, 0) == pkg.SDPA_ERR_DS_PATH                 # fp32
+    assert phase(1, 1, 64, 64) == pkg.SDPA_ERR_DS_PATH         # both sides <= 64
+    assert phase(3, 1) == pkg.SDPA_ERR_DS_PATH                 # no such phase
+    assert phase(-1, 1) == pkg.SDPA_ERR_DS_PATH
+    small = L.sdpa_hip_bwd_workspace_bytes_ds(1, 2, 64, 64, 128, 128, 1) - 1
+    assert phase(2, 1, ws=small) == pkg.SDPA_ERR_DS_PATH       # workspace one byte short
+    assert phase(2, 1, ws=0) == 22                             # below even the per-row workspace
+    assert phase(0, 1, B=0) == 0                               # empty: nothing to do
 
 
 def test_drop_threshold_values(pkg):

@@ -30,7 +30,8 @@ DTYPE_F16 = 1
 SDPA_OK = 0
 SDPA_ERR_HIP = 23
 SDPA_ERR_SCRATCH_LIMIT = 24
-_ARG_ERRORS = set(range(1, 23)) | {SDPA_ERR_SCRATCH_LIMIT}
+SDPA_ERR_DS_PATH = 25
+_ARG_ERRORS = set(range(1, 23)) | {SDPA_ERR_SCRATCH_LIMIT, SDPA_ERR_DS_PATH}
 
 _lib = None
 
@@ -83,6 +84,11 @@ def library():
     L.sdpa_hip_bwd_dkdv.restype = i32
     L.sdpa_hip_bwd_dkdv.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, sz, i32, i32, i32, i32,
                                     i32, f32, f32, i32, u64, u64, vp]
+    L.sdpa_hip_bwd_workspace_bytes_ds.restype = sz
+    L.sdpa_hip_bwd_workspace_bytes_ds.argtypes = [i32] * 7
+    L.sdpa_hip_bwd_ds_phase.restype = i32
+    L.sdpa_hip_bwd_ds_phase.argtypes = [i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, i32, i32,
+                                        i32, i32, i32, f32, f32, i32, u64, u64, vp]
     L.sdpa_hip_bwd_noalloc.restype = i32
     L.sdpa_hip_bwd_noalloc.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32,
                                        i32, i32, f32, f32, i32, u64, u64, vp]
@@ -191,8 +197,13 @@ def sdpa(q, k, v, seed=0, offset=0, dropout: float = 0.0, scale: float = 1.0,
 
 
 def sdpa_grad(q, k, v, o, stats, d_o, seed=0, offset=0, dropout: float = 0.0,
-              scale: float = 1.0, causal_mask: bool = False):
-    """Gradient op ``SdpaGrad`` (sdpa_ops.cc:34-63): returns ``(dq, dk, dv)``."""
+              scale: float = 1.0, causal_mask: bool = False, *, ds_path: bool = True):
+    """Gradient op ``SdpaGrad`` (sdpa_ops.cc:34-63): returns ``(dq, dk, dv)``.
+
+    ``ds_path``: give the backward the workspace of its dS path
+    (``sdpa_hip_bwd_workspace_bytes_ds``: float16 with a feature size over
+    64 then stores dS in the dK/dV kernel and forms dQ from it); False gives
+    it the per-row workspace only, and both kernels form dS."""
     import torch
     check_bwd(q, k, v, o, stats, d_o, seed, offset, causal_mask)
     if not (q.dtype == k.dtype == v.dtype == o.dtype == d_o.dtype):
@@ -208,7 +219,11 @@ def sdpa_grad(q, k, v, o, stats, d_o, seed=0, offset=0, dropout: float = 0.0,
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    ws_bytes = int(L.sdpa_hip_bwd_workspace_bytes(B, S_q))
+    if ds_path:
+        ws_bytes = int(L.sdpa_hip_bwd_workspace_bytes_ds(dt, B, S_q, S_kv, D_qk, D_v,
+                                                         int(bool(causal_mask))))
+    else:
+        ws_bytes = int(L.sdpa_hip_bwd_workspace_bytes(B, S_q))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
     rc = L.sdpa_hip_bwd(dt, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                         stats.data_ptr(), d_o.data_ptr(), dq.data_ptr(), dk.data_ptr(),

@@ -153,22 +153,57 @@ size_t sdpa_hip_bwd_workspace_bytes(int B, int S_q) {
 }  // extern "C"
 
 namespace {
-// Shared body of the three backward entry points.
-int bwd_entry(int phases, int dtype, const void* q, const void* k, const void* v, const void* o,
-              const float* stats, const void* d_o, void* dq, void* dk, void* dv, void* workspace,
-              size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v, float scale,
-              float dropout, int causal_mask, uint64_t seed, uint64_t offset, hipStream_t stream) {
+// The dS path's shapes: fp16 through the split dK/dV kernel, nothing empty.
+bool ds_shape(int dtype, int B, int S_q, int S_kv, int D_qk, int D_v) {
+    return dtype == SDPA_DTYPE_F16 && B > 0 && S_q > 0 && S_kv > 0 && D_qk > 0 && D_v > 0 &&
+           sdpa::bwd_ds_shape(D_qk, D_v);
+}
+}  // namespace
+
+extern "C" {
+
+size_t sdpa_hip_bwd_workspace_bytes_ds(int dtype, int B, int S_q, int S_kv, int D_qk, int D_v,
+                                       int causal_mask) {
+    const size_t rows = sdpa_hip_bwd_workspace_bytes(B, S_q);
+    if (!ds_shape(dtype, B, S_q, S_kv, D_qk, D_v) || D_qk > 128 || D_v > 128) return rows;
+    // the row values first (a multiple of 256 bytes), the stored dS after them
+    return rows + sdpa::DsLayout(S_q, S_kv, causal_mask != 0).bytes(B);
+}
+
+}  // extern "C"
+
+namespace {
+// Which launches a backward entry point makes:
+//   kRecompute -- `phases` of the path that forms dS in both kernels (dQ
+//                 first, it leaves the row values; then dK/dV);
+//   kAuto      -- all of it, by the dS path when the workspace allows;
+//   kDs0..2    -- one phase of the dS path (rows, dK/dV + dS, dQ).
+enum Mode { kRecompute, kAuto, kDs0, kDs1, kDs2 };
+
+// Shared body of the backward entry points.
+int bwd_entry(Mode mode, int phases, int dtype, const void* q, const void* k, const void* v,
+              const void* o, const float* stats, const void* d_o, void* dq, void* dk, void* dv,
+              void* workspace, size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
+              float scale, float dropout, int causal_mask, uint64_t seed, uint64_t offset,
+              hipStream_t stream) {
     int st = check_common(dtype, B, S_q, S_kv, D_qk, D_v, dropout, causal_mask);
     if (st != SDPA_OK) return st;
+    const bool ds_phase = mode == kDs0 || mode == kDs1 || mode == kDs2;
     if (B == 0) return SDPA_OK;
-    if (workspace_bytes < sdpa_hip_bwd_workspace_bytes(B, S_q)) return SDPA_ERR_WORKSPACE;
+    const size_t rows_bytes = sdpa_hip_bwd_workspace_bytes(B, S_q);
+    if (workspace_bytes < rows_bytes) return SDPA_ERR_WORKSPACE;
     const bool has_q = (size_t)S_q > 0, has_kv = (size_t)S_kv > 0;
-    const bool want_dq = phases & sdpa::kBwdDq, want_kv = phases & sdpa::kBwdDkDv;
-    if ((has_q && (!stats || !workspace)) || (has_q && D_qk > 0 && !q) ||
-        (has_q && D_v > 0 && !d_o) || (want_dq && has_q && D_qk > 0 && !dq) ||
-        (want_dq && has_q && D_v > 0 && !o) || (has_kv && D_qk > 0 && !k) ||
-        (has_kv && D_v > 0 && !v) || (want_kv && has_kv && D_qk > 0 && !dk) ||
-        (want_kv && has_kv && D_v > 0 && !dv))
+    // what the call computes (every launch of the dS path needs the rows of
+    // phase 0, so the full call checks all of its inputs)
+    const bool want_dq = ds_phase ? mode == kDs2 : (mode == kAuto || (phases & sdpa::kBwdDq));
+    const bool want_kv = ds_phase ? mode == kDs1 : (mode == kAuto || (phases & sdpa::kBwdDkDv));
+    const bool want_rows = ds_phase ? mode == kDs0 : want_dq;
+    if ((has_q && !workspace) || (has_q && !ds_phase && !stats) || (want_rows && has_q && !stats) ||
+        (has_q && D_qk > 0 && !q && (want_kv || !ds_phase)) ||
+        (has_q && D_v > 0 && !d_o && (want_kv || want_rows)) ||
+        (want_dq && has_q && D_qk > 0 && !dq) || (want_rows && has_q && D_v > 0 && !o) ||
+        (has_kv && D_qk > 0 && !k && (want_kv || want_dq)) || (has_kv && D_v > 0 && !v && (want_kv || !ds_phase)) ||
+        (want_kv && has_kv && D_qk > 0 && !dk) || (want_kv && has_kv && D_v > 0 && !dv))
         return SDPA_ERR_NULL_POINTER;
     sdpa::BwdParams p{};
     p.q = q;
@@ -182,13 +217,28 @@ int bwd_entry(int phases, int dtype, const void* q, const void* k, const void* v
     p.dv = dv;
     p.stats2 = static_cast<float*>(workspace);
     p.delta = static_cast<float*>(workspace) + (size_t)B * S_q;
+    p.ds = nullptr;
     p.s = sdpa::AttnShape{B, S_q, S_kv, D_qk, D_v};
     p.c = make_scalars(scale, dropout, causal_mask, seed, offset, true);
     const bool vec = vec_ok(dtype, D_qk, D_v,
-                            {q, k, v, d_o, want_dq ? o : nullptr, want_dq ? dq : nullptr,
+                            {q, k, v, d_o, want_rows ? o : nullptr, want_dq ? dq : nullptr,
                              want_kv ? dk : nullptr, want_kv ? dv : nullptr});
-    if (dtype == SDPA_DTYPE_F16 && vec) return hip_status(sdpa::launch_bwd_f16_dma(p, phases, stream));
-    return hip_status(sdpa::launch_bwd(p, (sdpa::DType)dtype, vec, phases, stream));
+    // the dS path: its shapes, aligned tensors, and the workspace for dS
+    const bool ds_ok = vec && ds_shape(dtype, B, S_q, S_kv, D_qk, D_v) &&
+                       workspace_bytes >= sdpa_hip_bwd_workspace_bytes_ds(dtype, B, S_q, S_kv, D_qk, D_v,
+                                                                          causal_mask);
+    if (ds_phase && !ds_ok) return SDPA_ERR_DS_PATH;
+    if (ds_phase || (mode == kAuto && ds_ok)) {
+        p.ds = static_cast<unsigned char*>(workspace) + rows_bytes;
+        hipError_t e = hipSuccess;
+        if (mode == kAuto || mode == kDs0) e = sdpa::launch_bwd_rows_f16(p, stream);
+        if (e == hipSuccess && (mode == kAuto || mode == kDs1)) e = sdpa::launch_bwd_dkdv_f16_split(p, stream);
+        if (e == hipSuccess && (mode == kAuto || mode == kDs2)) e = sdpa::launch_bwd_dq_ds_f16(p, stream);
+        return hip_status(e);
+    }
+    const int ph = mode == kAuto ? (sdpa::kBwdDq | sdpa::kBwdDkDv) : phases;
+    if (dtype == SDPA_DTYPE_F16 && vec) return hip_status(sdpa::launch_bwd_f16_dma(p, ph, stream));
+    return hip_status(sdpa::launch_bwd(p, (sdpa::DType)dtype, vec, ph, stream));
 }
 }  // namespace
 
@@ -199,9 +249,8 @@ int sdpa_hip_bwd(int dtype, const void* q, const void* k, const void* v, const v
                  void* workspace, size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk,
                  int D_v, float scale, float dropout, int causal_mask, uint64_t seed,
                  uint64_t offset, hipStream_t stream) {
-    return bwd_entry(sdpa::kBwdDq | sdpa::kBwdDkDv, dtype, q, k, v, o, stats, d_o, dq, dk, dv,
-                     workspace, workspace_bytes, B, S_q, S_kv, D_qk, D_v, scale, dropout,
-                     causal_mask, seed, offset, stream);
+    return bwd_entry(kAuto, 0, dtype, q, k, v, o, stats, d_o, dq, dk, dv, workspace, workspace_bytes, B,
+                     S_q, S_kv, D_qk, D_v, scale, dropout, causal_mask, seed, offset, stream);
 }
 
 int sdpa_hip_bwd_dq(int dtype, const void* q, const void* k, const void* v, const void* o,
@@ -209,9 +258,9 @@ int sdpa_hip_bwd_dq(int dtype, const void* q, const void* k, const void* v, cons
                     size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
                     float scale, float dropout, int causal_mask, uint64_t seed, uint64_t offset,
                     hipStream_t stream) {
-    return bwd_entry(sdpa::kBwdDq, dtype, q, k, v, o, stats, d_o, dq, nullptr, nullptr, workspace,
-                     workspace_bytes, B, S_q, S_kv, D_qk, D_v, scale, dropout, causal_mask, seed,
-                     offset, stream);
+    return bwd_entry(kRecompute, sdpa::kBwdDq, dtype, q, k, v, o, stats, d_o, dq, nullptr, nullptr,
+                     workspace, workspace_bytes, B, S_q, S_kv, D_qk, D_v, scale, dropout, causal_mask,
+                     seed, offset, stream);
 }
 
 int sdpa_hip_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, const float* stats,
@@ -219,9 +268,20 @@ int sdpa_hip_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, co
                       size_t workspace_bytes, int B, int S_q, int S_kv, int D_qk, int D_v,
                       float scale, float dropout, int causal_mask, uint64_t seed,
                       uint64_t offset, hipStream_t stream) {
-    return bwd_entry(sdpa::kBwdDkDv, dtype, q, k, v, nullptr, stats, d_o, nullptr, dk, dv,
+    return bwd_entry(kRecompute, sdpa::kBwdDkDv, dtype, q, k, v, nullptr, stats, d_o, nullptr, dk, dv,
                      const_cast<void*>(workspace), workspace_bytes, B, S_q, S_kv, D_qk, D_v, scale,
                      dropout, causal_mask, seed, offset, stream);
+}
+
+int sdpa_hip_bwd_ds_phase(int phase, int dtype, const void* q, const void* k, const void* v,
+                          const void* o, const float* stats, const void* d_o, void* dq, void* dk,
+                          void* dv, void* workspace, size_t workspace_bytes, int B, int S_q,
+                          int S_kv, int D_qk, int D_v, float scale, float dropout, int causal_mask,
+                          uint64_t seed, uint64_t offset, hipStream_t stream) {
+    if (phase < 0 || phase > 2) return SDPA_ERR_DS_PATH;
+    const Mode m = phase == 0 ? kDs0 : (phase == 1 ? kDs1 : kDs2);
+    return bwd_entry(m, 0, dtype, q, k, v, o, stats, d_o, dq, dk, dv, workspace, workspace_bytes, B, S_q,
+                     S_kv, D_qk, D_v, scale, dropout, causal_mask, seed, offset, stream);
 }
 
 }  // extern "C"
@@ -276,7 +336,7 @@ int sdpa_hip_bwd_noalloc(int dtype, const void* q, const void* k, const void* v,
     }
     // The kernels write every workspace row before reading it (dQ kernel,
     // then dK/dV kernel on the same stream): nothing needs clearing.
-    return bwd_entry(sdpa::kBwdDq | sdpa::kBwdDkDv, dtype, q, k, v, o, stats, d_o, dq, dk, dv, ws,
+    return bwd_entry(kRecompute, sdpa::kBwdDq | sdpa::kBwdDkDv, dtype, q, k, v, o, stats, d_o, dq, dk, dv, ws,
                      need, B, S_q, S_kv, D_qk, D_v, scale, dropout, causal_mask, seed, offset,
                      stream);
 }

@@ -41,6 +41,9 @@ inline const char* status_message(int status) {
         case SDPA_ERR_HIP: return "HIP runtime error";
         case SDPA_ERR_SCRATCH_LIMIT:
             return "B * S_q exceeds the static scratch of sdpa_hip_bwd_noalloc (2097152 query rows)";
+        case SDPA_ERR_DS_PATH:
+            return "the dS path of the backward needs float16, a feature size over 64, 16-byte aligned tensors "
+                   "and a workspace of sdpa_hip_bwd_workspace_bytes_ds bytes";
         default: return "unknown sdpa status";
     }
 }

@@ -26,6 +26,11 @@
 namespace sdpa {
 namespace {
 
+// The P role hands P to the dS role (and into its own dV product) as fp16
+// x = P 2^kXShift: P ranges over [1e-6, 1] (the gate below, the row
+// statistics above), and 2^6 puts all of it in fp16's normal range.
+constexpr float kXScale = 64.f;  // 2^kXShift, kXShift = 6
+
 // ===========================================================================
 // Backward, dK/dV kernel with the work of a key split over two waves
 // ===========================================================================
@@ -35,7 +40,7 @@ namespace {
 //                          (stats2 carries the shift; see kGateShift), P~ = P * keep,
 //                          dV^T += dO^T P~; it hands P to wave w + 4 through
 //                          LDS with the dropout decision in the sign (-P for a
-//                          dropped element);
+//                          dropped element), as fp16 P 2^kXShift (kXScale);
 //   wave w + 4  (dS role): dP = dO V^T, dS = P (keep ? dP ksc - delta : -delta),
 //                          dK^T += Q^T dS, one block behind the P role.
 // Each role holds one operand (K or V, 32 VGPRs) and one accumulator (64), so
@@ -62,7 +67,7 @@ struct DkvSplitCfg {
     static_assert(LDS_BYTES <= 160 * 1024, "gfx950 LDS");
 };
 
-template <int DQK, int DV, bool CAUSAL, bool DROP>
+template <int DQK, int DV, bool CAUSAL, bool DROP, bool DS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
     using Cfg = DkvSplitCfg<DQK, DV>;
@@ -173,8 +178,10 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
                 for (int e = 0; e < 4; ++e) {
                     float x = __builtin_fmaf(sacc[4 * g + e], sl2, -st4[g][e]);
                     if (MASK && ((CAUSAL && kd > 8 * g + e) || 8 * g + e >= qd)) x = -INFINITY;
-                    // stats2 carries kGateShift: exp2 gives P' (0 where P <= 1e-6)
-                    const float pe = fast_exp2(x) * kGateScale;
+                    // stats2 carries kGateShift: exp2 gives P' (0 where P <= 1e-6);
+                    // x = P 2^kXShift keeps every P above the gate in fp16's
+                    // normal range (2^-11 relative, not a subnormal's spacing)
+                    const float pe = fast_exp2(x) * (kGateScale * kXScale);
                     if constexpr (DROP)
                         x4[e] = lcg_keep(st_sub + (uint64_t)(8 * g + e) * row_step, thr) ? pe : -pe;
                     else
@@ -325,8 +332,10 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
         __syncthreads();
         if (key_ok) {
             half_t* dVb = static_cast<half_t*>(p.dv) + ((size_t)b * S_kv + my_k) * D_v;
-            if (D_v == DV) store_rows_f16<DV>(dVb, dvacc, p.c.keep_scale, hh);
-            else store_rows_f16_n<DV>(dVb, dvacc, p.c.keep_scale, hh, D_v);
+            // dV was accumulated from x = P~ 2^kXShift
+            const float fv = p.c.keep_scale * (1.f / kXScale);
+            if (D_v == DV) store_rows_f16<DV>(dVb, dvacc, fv, hh);
+            else store_rows_f16_n<DV>(dVb, dvacc, fv, hh, D_v);
         }
     } else {
         // ----------------------------------------------------------- dS role
@@ -373,13 +382,13 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
         floatx16 dkacc[DQK / 32];
 #pragma unroll
         for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};
+        const DsLayout dsl(S_q, S_kv, CAUSAL);
 
         // dS' of one sub-tile from dP, delta' and the P role's x.
         auto elem = [&](const floatx16& dpacc, const floatx4 (&de4)[4], const half8& xv0, const half8& xv1,
                         half8& ds0, half8& ds1) {
             // dS' = P (keep ? dP - delta' : -delta') = max(x, 0) dP - |x| delta'
-            const half8 xm0 = DROP ? relu_h8(xv0) : xv0;
-            const half8 xm1 = DROP ? relu_h8(xv1) : xv1;
+            // (x 2^-kXShift: exact)
             uint32_t wd[8];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -387,8 +396,8 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int r = 4 * g + e;
-                    const float xq = (float)(r < 8 ? xv0[r] : xv1[r - 8]);
-                    const float mq = (float)(r < 8 ? xm0[r] : xm1[r - 8]);
+                    const float xq = (float)(r < 8 ? xv0[r] : xv1[r - 8]) * (1.f / kXScale);
+                    const float mq = DROP ? fmaxf(xq, 0.f) : xq;
                     if constexpr (DROP)
                         ds4[e] = __builtin_fmaf(-__builtin_fabsf(xq), de4[g][e], mq * dpacc[r]);
                     else
@@ -422,6 +431,15 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
             __builtin_amdgcn_sched_barrier(0);
             half8 ds0, ds1;
             elem(dpacc, de4, xv0, xv1, ds0, ds1);
+            if constexpr (DS) {
+                // dS' of this sub-tile into its chunk (DsLayout): this lane's
+                // key row, its 16 queries as the two halves of its 32 bytes
+                const int qb = (q_top - m * BQ) / BQ;
+                unsigned char* dst = static_cast<unsigned char*>(p.ds) + dsl.offset(b, kt, qb) + t * 8192 +
+                                     (32 * kw + l32) * 64 + hh * 32;
+                *reinterpret_cast<half8*>(dst) = ds0;
+                *reinterpret_cast<half8*>(dst + 16) = ds1;
+            }
 #pragma unroll
             for (int dt = 0; dt < DQK / 32; ++dt) {
                 dkacc[dt] = mfma_f16(at[0][dt], ds0, dkacc[dt]);
@@ -496,10 +514,14 @@ hipError_t launch_bwd_dkdv_f16_split(const BwdParams& p, hipStream_t stream) {
                     constexpr bool CA = decltype(c)::value, DR = decltype(d)::value;
                     if constexpr (DQK == 128 || DV == 128) {
                         using CS = DkvSplitCfg<DQK, DV>;
+                        static_assert(CS::BKV == DsLayout::KT && CS::BQ == DsLayout::QBK, "dS chunk geometry");
                         const long long n = (long long)((S_kv + CS::BKV - 1) / CS::BKV) * B;
-                        return launch_kernel<sdpa_bwd_dkdv_f16_split_kernel<DQK, DV, CA, DR>>(
-                            (unsigned)n, CS::NT, CS::LDS_BYTES, stream, p,
-                            row_window((size_t)p.s.S_q * (DQK + DV) * 2));
+                        const int win = row_window((size_t)p.s.S_q * (DQK + DV) * 2);
+                        if (p.ds)
+                            return launch_kernel<sdpa_bwd_dkdv_f16_split_kernel<DQK, DV, CA, DR, true>>(
+                                (unsigned)n, CS::NT, CS::LDS_BYTES, stream, p, win);
+                        return launch_kernel<sdpa_bwd_dkdv_f16_split_kernel<DQK, DV, CA, DR, false>>(
+                            (unsigned)n, CS::NT, CS::LDS_BYTES, stream, p, win);
                     } else {
                         return hipErrorInvalidValue;  // the one-wave kernel serves D <= 64
                     }

@@ -1,0 +1,215 @@
+// sdpa_f16_dq_ds.hip -- the dS path of the fp16 SdpaGrad for gfx950: dQ as a
+// product with the dS' the dK/dV kernel stored, instead of a kernel that
+// forms S, P, dP and dS once more.
+//
+// Order of the path (sdpa_capi.hip):
+//   1. row kernel  -- stats2 and delta per query row into the workspace (the
+//                     values the dQ kernel of the other path writes first);
+//   2. dK/dV       -- the split-role kernel (sdpa_f16_dkdv_split.hip) with
+//                     p.ds set: its dS role stores every dS' it forms;
+//   3. dQ          -- dQ^T = K^T dS'^T per 32 queries, scaled once at the store.
+// dQ then costs one fp16 read of dS' (2 bytes per visited score) instead of
+// three products and the element-wise work per score; the dS' it reads are
+// the ones dK was formed from.
+//
+// Element semantics (sdpa/sdpa_bwd.cu.cc:291-327): dQ_i = scale sum_j dS_ij
+// K_j, with dS as the dK/dV kernel forms it (P from the fp16 P of its P role,
+// the 1e-6 gate, the dropout decision; with dropout dS' = dS (1-p), scaled
+// back by 1/(1-p) at the store).
+#include <type_traits>
+
+#include "sdpa_dma.h"
+#include "sdpa_launch.h"
+#include "sdpa_params.h"
+
+namespace sdpa {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Row values.  One lane pair per query row (lane = row, hh = half of the
+// features): delta = sum_d dO O in the order of the dQ kernel's prologue, and
+// stats2 = stats log2(e) + kGateShift as one fma, so that both paths hand the
+// dK/dV kernel the same values.
+// ---------------------------------------------------------------------------
+template <int DV>
+__global__ __launch_bounds__(256) void sdpa_bwd_rows_f16_kernel(const BwdParams p) {
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5, wave = tid >> 6;
+    const int S_q = p.s.S_q, D_v = p.s.D_v;
+    const int tiles = (S_q + 127) / 128;
+    const int b = (int)(blockIdx.x / (unsigned)tiles), qt = (int)(blockIdx.x % (unsigned)tiles);
+    const int my_q = qt * 128 + 32 * wave + l32;
+    const half_t* Ob = static_cast<const half_t*>(p.o) + (size_t)b * S_q * D_v;
+    const half_t* dOb = static_cast<const half_t*>(p.d_o) + (size_t)b * S_q * D_v;
+    float dpart = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < DV / 16; ++ks) {
+        const half8 d8 = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(dOb, my_q, S_q, 16 * ks + 8 * hh, D_v, D_v));
+        const half8 o8 = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Ob, my_q, S_q, 16 * ks + 8 * hh, D_v, D_v));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dpart += (float)d8[e] * (float)o8[e];
+    }
+    const float delta = xhalf_sum(dpart);
+    if (my_q < S_q && hh == 0) {
+        const size_t row_q = (size_t)b * S_q + my_q;
+        p.delta[row_q] = delta;
+        p.stats2[row_q] = __builtin_fmaf(p.stats[row_q], kLog2e, kGateShift);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dQ from the stored dS'.  Four waves of 32 queries (128 per workgroup); key
+// steps of 64 through a two-stage LDS ring.  A stage holds the K tile (read
+// transposed: the A operand K^T) and each wave's own dS' tile, 64 keys x 32
+// queries as stored (read transposed: the B operand dS'^T, lane = query).
+// The lanes of a wave take the queries in the stored order (DsLayout), so the
+// tile is copied as it lies; lane l32 owns query qw0 + pi(l32).
+// ---------------------------------------------------------------------------
+template <int DQK>
+struct DqDsCfg {
+    static constexpr int NW = 4, NT = 64 * NW, BM = 32 * NW, BN = 64;
+    static constexpr int LK = DQK / 8;
+    static constexpr int KB = BN * DQK * 2;  // K tile
+    static constexpr int SB = BN * 64;       // one wave's dS' tile
+    static constexpr int STAGE = KB + NW * SB;
+    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+    static_assert(2 * LDS_BYTES <= 160 * 1024, "two workgroups per CU");
+};
+
+template <int DQK, bool CAUSAL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void sdpa_bwd_dq_ds_f16_kernel(const BwdParams p, const int win) {
+    using Cfg = DqDsCfg<DQK>;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, NW = Cfg::NW, NDT = DQK / 32;
+    static_assert(BN * 2 == DsLayout::KT && BM % DsLayout::QBK == 0, "steps tile the stored chunks");
+
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int B = p.s.B, S_q = p.s.S_q, S_kv = p.s.S_kv, D_qk = p.s.D_qk;
+    const int tiles = (S_q + BM - 1) / BM;
+    int b, qt;
+    xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, win, b, qt);
+    const int q0 = qt * BM, qw0 = q0 + 32 * wave;
+    const int my_q = qw0 + 8 * ((l32 >> 2) & 3) + 4 * (l32 >> 4) + (l32 & 3);
+    const bool live = qw0 < S_q;
+    const DsLayout dsl(S_q, S_kv, CAUSAL);
+    const int qb = qw0 / DsLayout::QBK, tq = (qw0 / 32) & 1;
+    const unsigned char* dsb = static_cast<const unsigned char*>(p.ds);
+
+    // Sub-tile g (keys kv0 + 32 g ..) of this wave: stored by the dK/dV
+    // kernel under the same predicate (its sub_live); a stored sub-tile lies
+    // in a visited chunk (keys from kt 128 up to query qw0 + 31 put qw0 in a
+    // block at or past qbb(kt)).
+    auto sub_live = [&](int kv0, int g) {
+        const int kw0 = kv0 + 32 * g;
+        return live && kw0 < S_kv && !(CAUSAL && qw0 + 31 < kw0);
+    };
+
+    const RowSrc ksrc = row_src(p.k, (size_t)b * S_kv, S_kv, D_qk * 2);
+    TileCopy<BN, LK, NW, true> kc;
+    kc.init(wave, lane, D_qk * 2, D_qk / 8);
+    TileCopy<BN, 4, 1, true> sc;  // 64 rows of 64 bytes: a plain 4 KB copy
+    sc.init(0, lane, 64, 4);
+    const uint32_t lds0 = lds_base();
+    const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
+    const int nsteps = (kv_end + BN - 1) / BN;
+    // Copies of step `step` into stage step & 1: the wave's share of the K
+    // tile and, when its first sub-tile is live (the second is live only with
+    // the first), its dS' rows.
+    auto issue = [&](int step) {
+        const int kv0 = step * BN;
+        const uint32_t so = (uint32_t)((step & 1) * Cfg::STAGE);
+        kc.issue(ksrc.shifted(kv0), lds0 + so + 1024u * (uint32_t)wave, wave);
+        if (sub_live(kv0, 0)) {
+            const unsigned char* src =
+                dsb + dsl.offset(b, kv0 / DsLayout::KT, qb) + tq * 8192 + (kv0 % DsLayout::KT) * 64;
+            sc.issue(RowSrc{uniform_ptr(src), BN, 64, 0x7FFFFFFF / 64},
+                     lds0 + so + (uint32_t)(Cfg::KB + Cfg::SB * wave), 0);
+        }
+    };
+
+    floatx16 acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx16{};
+    const uint32_t kl = lds0 + tr_lane_off<LK>(lane);                                   // K^T
+    const uint32_t sl = lds0 + (uint32_t)(Cfg::KB + Cfg::SB * wave) + tr_lane_off<4>(lane);  // dS'^T
+
+    // One 32-key sub-tile: two 16-key halves, NDT products each.  Element i
+    // of a transposed read (two ds_read_b64_tr_b16 of four rows each) holds
+    // row R0 + 8 (i / 4) + 4 hh + i % 4, for the K^T and the dS'^T operand
+    // alike.  PART: keys past S_kv (whose K rows read as zero) get a zero dS'
+    // as well.
+    auto sub = [&]<bool PART>(uint32_t so, int kv0, int g) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int R0 = 32 * g + 16 * j;
+            half8 bs = ld_tr8(sl + so + 64u * R0, sl + so + 64u * (R0 + 8));
+            if constexpr (PART) {
+                const int lim = S_kv - (kv0 + R0 + 4 * hh);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (8 * (i >> 2) + (i & 3) >= lim) bs[i] = (half_t)0.f;
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const uint32_t a = (kl ^ (uint32_t)(64 * dt)) + so;
+                const half8 ak = ld_tr8(a + 16u * LK * R0, a + 16u * LK * (R0 + 8));
+                acc[dt] = mfma_f16(ak, bs, acc[dt]);
+            }
+        }
+    };
+
+    if (nsteps > 0) issue(0);
+    for (int step = 0; step < nsteps; ++step) {
+        wait_vm();
+        __syncthreads();
+        if (step + 1 < nsteps) issue(step + 1);
+        const int kv0 = step * BN;
+        const uint32_t so = (uint32_t)((step & 1) * Cfg::STAGE);
+        const bool part = kv0 + BN > S_kv;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            if (!sub_live(kv0, g)) continue;
+            if (part) sub.template operator()<true>(so, kv0, g);
+            else sub.template operator()<false>(so, kv0, g);
+        }
+    }
+
+    if (live && my_q < S_q) {
+        // dS' = dS (1-p) with dropout (keep_scale 1/(1-p)); every element
+        // dropped (keep_scale 0): dS' = dS
+        const float f = (p.c.use_dropout && p.c.keep_scale != 0.f) ? p.c.scale * p.c.keep_scale : p.c.scale;
+        half_t* dQb = static_cast<half_t*>(p.dq) + ((size_t)b * S_q + my_q) * D_qk;
+        if (D_qk == DQK) store_rows_f16<DQK>(dQb, acc, f, hh);
+        else store_rows_f16_n<DQK>(dQb, acc, f, hh, D_qk);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_bwd_rows_f16(const BwdParams& p, hipStream_t stream) {
+    const int B = p.s.B, S_q = p.s.S_q;
+    if (B == 0 || S_q == 0) return hipSuccess;
+    const long long n = (long long)((S_q + 127) / 128) * B;
+    if (n > 0x7FFFFFFFLL) return hipErrorInvalidValue;
+    return with_dim(p.s.D_v, [&](auto dv) {
+        constexpr int DV = decltype(dv)::value;
+        return launch_kernel<sdpa_bwd_rows_f16_kernel<DV>>((unsigned)n, 256, 0, stream, p);
+    });
+}
+
+hipError_t launch_bwd_dq_ds_f16(const BwdParams& p, hipStream_t stream) {
+    const int B = p.s.B, S_q = p.s.S_q;
+    if (B == 0 || S_q == 0) return hipSuccess;
+    if (!p.ds) return hipErrorInvalidValue;
+    return with_dim(p.s.D_qk, [&](auto dqk) {
+        return with_bool(p.c.causal != 0, [&](auto c) {
+            constexpr int DQK = decltype(dqk)::value;
+            using Cfg = DqDsCfg<DQK>;
+            const long long n = (long long)((S_q + Cfg::BM - 1) / Cfg::BM) * B;
+            return launch_kernel<sdpa_bwd_dq_ds_f16_kernel<DQK, decltype(c)::value>>(
+                (unsigned)n, Cfg::NT, Cfg::LDS_BYTES, stream, p, row_window((size_t)p.s.S_kv * DQK * 2));
+        });
+    });
+}
+
+}  // namespace sdpa

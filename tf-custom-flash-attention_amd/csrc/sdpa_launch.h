@@ -63,7 +63,14 @@ hipError_t launch_bwd_f16_dma(const BwdParams& p, int phases, hipStream_t stream
 // dQ phase of launch_bwd_f16_dma (sdpa_f16_dq.hip)
 hipError_t launch_bwd_dq_f16_dma(const BwdParams& p, hipStream_t stream);
 // dK/dV phase of launch_bwd_f16_dma at a 128-wide side (D_qk or D_v = 128;
-// sdpa_f16_dkdv_split.hip)
+// sdpa_f16_dkdv_split.hip); with p.ds set it also stores dS' (DsLayout)
 hipError_t launch_bwd_dkdv_f16_split(const BwdParams& p, hipStream_t stream);
+
+// dS path of the fp16 DMA backward (sdpa_f16_dq_ds.hip), for the shapes the
+// split dK/dV kernel serves: the row values (stats2, delta), then
+// launch_bwd_dkdv_f16_split with p.ds, then dQ from the stored dS'.
+inline bool bwd_ds_shape(int D_qk, int D_v) { return D_qk > 64 || D_v > 64; }
+hipError_t launch_bwd_rows_f16(const BwdParams& p, hipStream_t stream);
+hipError_t launch_bwd_dq_ds_f16(const BwdParams& p, hipStream_t stream);
 
 }  // namespace sdpa

@@ -6,6 +6,8 @@
 
 #include <stdint.h>
 
+#include <hip/hip_runtime.h>
+
 namespace sdpa {
 
 struct AttnShape {
@@ -43,11 +45,45 @@ struct BwdParams {
     void* dq;
     void* dk;
     void* dv;
-    // Workspace, written by the dQ kernel and read by the dK/dV kernel:
+    // Workspace, written by the dQ kernel (or the row kernel of the dS path)
+    // and read by the dK/dV kernel:
     float* stats2;  // [B, S_q]: stats_i * log2(e) + kGateShift (sdpa_device.h)
     float* delta;   // [B, S_q]: delta_i = sum_d dO[i,d] * O[i,d]
+    // dS path only (else null): dS' of every visited (key tile, query block),
+    // written by the dK/dV kernel and read by the dQ kernel (DsLayout)
+    void* ds;
     AttnShape s;
     AttnScalars c;
+};
+
+// Layout of the stored dS' of the fp16 dS path.  The dK/dV kernel walks key
+// tiles of 128 keys; under the causal mask key tile kt visits the query
+// blocks (64 queries) qb >= qbb(kt) = min(128 kt, S_q) / 64, else all of
+// them.  Each visited (kt, qb) is a 16 KB chunk, and the chunks of a batch
+// row follow each other kt-major, qb-minor.  Inside a chunk: two 32-query
+// sub-tiles t, each [128 keys][32 queries] fp16 (64 bytes per key), the 32
+// queries in the order the dK/dV kernel's lanes hold them: position j is
+// query 8 ((j >> 2) & 3) + 4 (j >> 4) + (j & 3) of the sub-tile.
+struct DsLayout {
+    static constexpr int KT = 128, QBK = 64, CHUNK = 16384;
+    int S_q, QB, F, tiles;
+    bool causal;
+    __host__ __device__ DsLayout(int S_q_, int S_kv, bool causal_)
+        : S_q(S_q_), QB((S_q_ + QBK - 1) / QBK), F(S_q_ / QBK), tiles((S_kv + KT - 1) / KT), causal(causal_) {}
+    // first query block key tile kt visits
+    __host__ __device__ int qbb(int kt) const { return !causal ? 0 : ((long long)KT * kt <= S_q ? 2 * kt : F); }
+    // chunks of the key tiles before kt
+    __host__ __device__ long long prefix(int kt) const {
+        if (!causal) return (long long)kt * QB;
+        const long long J = kt < S_q / KT + 1 ? kt : S_q / KT + 1;  // tiles j < kt with 128 j <= S_q
+        return J * QB - J * (J - 1) + (long long)(kt - J) * (QB - F);
+    }
+    __host__ __device__ long long per_row() const { return prefix(tiles); }
+    // byte offset of chunk (b, kt, qb), qb >= qbb(kt)
+    __host__ __device__ size_t offset(int b, int kt, int qb) const {
+        return ((size_t)b * (size_t)per_row() + (size_t)prefix(kt) + (size_t)(qb - qbb(kt))) * CHUNK;
+    }
+    __host__ __device__ size_t bytes(int B) const { return (size_t)B * (size_t)per_row() * CHUNK; }
 };
 
 }  // namespace sdpa
