@@ -90,11 +90,18 @@ struct Backend<GPUDevice> {
                       const float* stats, const void* d_o, void* dq, void* dk, void* dv, int B, int S_q,
                       int S_kv, int D_qk, int D_v, float scale, float dropout, bool causal, uint64 seed,
                       uint64 offset) {
-        // per-query-row workspace of the two backward kernels, from TF's allocator
-        const size_t ws_bytes = sdpa_hip_bwd_workspace_bytes(B, S_q);
+        // Workspace from TF's allocator: the dS path's (the per-row values and
+        // the stored dS, fp16 at a feature size over 64) when it can be had,
+        // else the per-row one (both backward kernels then form dS).
+        size_t ws_bytes = sdpa_hip_bwd_workspace_bytes_ds(dt, B, S_q, S_kv, D_qk, D_v, causal ? 1 : 0);
         Tensor ws;
-        TF_RETURN_IF_ERROR(ctx->allocate_temp(
-            DT_UINT8, TensorShape({static_cast<int64_t>(std::max<size_t>(ws_bytes, 1))}), &ws));
+        Status st = ctx->allocate_temp(
+            DT_UINT8, TensorShape({static_cast<int64_t>(std::max<size_t>(ws_bytes, 1))}), &ws);
+        if (!st.ok()) {
+            ws_bytes = sdpa_hip_bwd_workspace_bytes(B, S_q);
+            TF_RETURN_IF_ERROR(ctx->allocate_temp(
+                DT_UINT8, TensorShape({static_cast<int64_t>(std::max<size_t>(ws_bytes, 1))}), &ws));
+        }
         return FromSdpa(sdpa_hip_bwd(dt, q, k, v, o, stats, d_o, dq, dk, dv, ws.flat<uint8>().data(), ws_bytes,
                                      B, S_q, S_kv, D_qk, D_v, scale, dropout, causal, seed, offset,
                                      stream(ctx)));
