@@ -433,7 +433,12 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
             elem(dpacc, de4, xv0, xv1, ds0, ds1);
             if constexpr (DS) {
                 // dS' of this sub-tile into its chunk (DsLayout): this lane's
-                // key row, its 16 queries as the two halves of its 32 bytes
+                // key row, its 16 queries as the two halves of its 32 bytes;
+                // zero for keys past S_kv (the dQ kernel reads them unmasked)
+                if (kw0 + 31 >= S_kv && !key_ok) {
+                    ds0 = half8{};
+                    ds1 = half8{};
+                }
                 const int qb = (q_top - m * BQ) / BQ;
                 unsigned char* dst = static_cast<unsigned char*>(p.ds) + dsl.offset(b, kt, qb) + t * 8192 +
                                      (32 * kw + l32) * 64 + hh * 32;

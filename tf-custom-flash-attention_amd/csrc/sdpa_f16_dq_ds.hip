@@ -57,21 +57,23 @@ __global__ __launch_bounds__(256) void sdpa_bwd_rows_f16_kernel(const BwdParams 
 }
 
 // ---------------------------------------------------------------------------
-// dQ from the stored dS'.  Four waves of 32 queries (128 per workgroup); key
-// steps of 64 through a two-stage LDS ring.  A stage holds the K tile (read
-// transposed: the A operand K^T) and each wave's own dS' tile, 64 keys x 32
-// queries as stored (read transposed: the B operand dS'^T, lane = query).
-// The lanes of a wave take the queries in the stored order (DsLayout), so the
-// tile is copied as it lies; lane l32 owns query qw0 + pi(l32).
+// dQ from the stored dS'.  Four waves of 64 queries (256 per workgroup): a
+// wave owns one stored query block (its two 32-query sub-tiles), so every
+// K^T operand it reads from LDS feeds two MFMAs.  Key steps of 32 (one stored
+// key group) through a three-stage LDS ring of the K tile (read transposed:
+// the A operand K^T) and each wave's two dS' tiles, 32 keys x 32 queries as
+// stored (read transposed: the B operand dS'^T, lane = query).  The lanes of
+// a wave take the queries in the stored order (DsLayout), so the tiles are
+// copied as they lie; lane l32 owns queries qb 64 + 32 t + pi(l32).
 // ---------------------------------------------------------------------------
 template <int DQK>
 struct DqDsCfg {
-    static constexpr int NW = 4, NT = 64 * NW, BM = 32 * NW, BN = 64;
+    static constexpr int NW = 4, NT = 64 * NW, BM = 64 * NW, BN = 32, NSTAGE = 3;
     static constexpr int LK = DQK / 8;
     static constexpr int KB = BN * DQK * 2;  // K tile
-    static constexpr int SB = BN * 64;       // one wave's dS' tile
-    static constexpr int STAGE = KB + NW * SB;
-    static constexpr size_t LDS_BYTES = 2 * (size_t)STAGE;
+    static constexpr int SB = BN * 64;       // one 32-query dS' tile
+    static constexpr int STAGE = KB + 2 * NW * SB;
+    static constexpr size_t LDS_BYTES = NSTAGE * (size_t)STAGE;
     static_assert(2 * LDS_BYTES <= 160 * 1024, "two workgroups per CU");
 };
 
@@ -79,8 +81,8 @@ template <int DQK, bool CAUSAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_bwd_dq_ds_f16_kernel(const BwdParams p, const int win) {
     using Cfg = DqDsCfg<DQK>;
-    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, NW = Cfg::NW, NDT = DQK / 32;
-    static_assert(BN * 2 == DsLayout::KT && BM % DsLayout::QBK == 0, "steps tile the stored chunks");
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, NW = Cfg::NW, NSTAGE = Cfg::NSTAGE, NDT = DQK / 32;
+    static_assert(DsLayout::KT % BN == 0 && BM % DsLayout::QBK == 0, "steps tile the stored chunks");
 
     const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -88,99 +90,114 @@ void sdpa_bwd_dq_ds_f16_kernel(const BwdParams p, const int win) {
     const int tiles = (S_q + BM - 1) / BM;
     int b, qt;
     xcd_map(blockIdx.x, B * tiles, tiles, CAUSAL, win, b, qt);
-    const int q0 = qt * BM, qw0 = q0 + 32 * wave;
-    const int my_q = qw0 + 8 * ((l32 >> 2) & 3) + 4 * (l32 >> 4) + (l32 & 3);
-    const bool live = qw0 < S_q;
+    const int q0 = qt * BM, qw0 = q0 + 64 * wave, qb = qw0 / DsLayout::QBK;
+    const int pq = 8 * ((l32 >> 2) & 3) + 4 * (l32 >> 4) + (l32 & 3);  // stored position -> query
     const DsLayout dsl(S_q, S_kv, CAUSAL);
-    const int qb = qw0 / DsLayout::QBK, tq = (qw0 / 32) & 1;
     const unsigned char* dsb = static_cast<const unsigned char*>(p.ds);
 
-    // Sub-tile g (keys kv0 + 32 g ..) of this wave: stored by the dK/dV
-    // kernel under the same predicate (its sub_live); a stored sub-tile lies
-    // in a visited chunk (keys from kt 128 up to query qw0 + 31 put qw0 in a
-    // block at or past qbb(kt)).
-    auto sub_live = [&](int kv0, int g) {
-        const int kw0 = kv0 + 32 * g;
-        return live && kw0 < S_kv && !(CAUSAL && qw0 + 31 < kw0);
+    // Sub-tile t (queries qw0 + 32 t ..) at the key group kv0: stored by the
+    // dK/dV kernel under the same predicate (its sub_live), and then in a
+    // visited chunk (keys from kt 128 up to query qw0 + 32 t + 31 put the
+    // query block at or past qbb(kt)).  Under the causal mask either may be
+    // live without the other (the group at qw0 + 32 reaches sub-tile 1 only).
+    auto sub_live = [&](int kv0, int t) {
+        const int qs = qw0 + 32 * t;
+        return qs < S_q && kv0 < S_kv && !(CAUSAL && qs + 31 < kv0);
     };
 
     const RowSrc ksrc = row_src(p.k, (size_t)b * S_kv, S_kv, D_qk * 2);
     TileCopy<BN, LK, NW, true> kc;
     kc.init(wave, lane, D_qk * 2, D_qk / 8);
-    TileCopy<BN, 4, 1, true> sc;  // 64 rows of 64 bytes: a plain 4 KB copy
+    TileCopy<BN, 4, 1, true> sc;  // 32 rows of 64 bytes: a plain 2 KB copy
     sc.init(0, lane, 64, 4);
     const uint32_t lds0 = lds_base();
     const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
     const int nsteps = (kv_end + BN - 1) / BN;
-    // Copies of step `step` into stage step & 1: the wave's share of the K
-    // tile and, when its first sub-tile is live (the second is live only with
-    // the first), its dS' rows.
+    // Copies of step `step` into stage step % NSTAGE: the wave's share of the
+    // K tile and its live dS' tiles.  Returns the number of copies issued.
     auto issue = [&](int step) {
         const int kv0 = step * BN;
-        const uint32_t so = (uint32_t)((step & 1) * Cfg::STAGE);
+        const uint32_t so = (uint32_t)((step % NSTAGE) * Cfg::STAGE);
         kc.issue(ksrc.shifted(kv0), lds0 + so + 1024u * (uint32_t)wave, wave);
-        if (sub_live(kv0, 0)) {
-            const unsigned char* src =
-                dsb + dsl.offset(b, kv0 / DsLayout::KT, qb) + tq * 8192 + (kv0 % DsLayout::KT) * 64;
-            sc.issue(RowSrc{uniform_ptr(src), BN, 64, 0x7FFFFFFF / 64},
-                     lds0 + so + (uint32_t)(Cfg::KB + Cfg::SB * wave), 0);
+        int n = decltype(kc)::count(wave);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (sub_live(kv0, t)) {
+                const unsigned char* src = dsb + dsl.offset(b, kv0 / DsLayout::KT, qb) + t * 8192 +
+                                           (kv0 % DsLayout::KT) * 64;
+                sc.issue(RowSrc{uniform_ptr(src), BN, 64, 0x7FFFFFFF / 64},
+                         lds0 + so + (uint32_t)(Cfg::KB + Cfg::SB * (2 * wave + t)), 0);
+                n += decltype(sc)::count(0);
+            }
         }
+        return n;
     };
 
-    floatx16 acc[NDT];
+    floatx16 acc[2][NDT];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx16{};
-    const uint32_t kl = lds0 + tr_lane_off<LK>(lane);                                   // K^T
-    const uint32_t sl = lds0 + (uint32_t)(Cfg::KB + Cfg::SB * wave) + tr_lane_off<4>(lane);  // dS'^T
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[t][dt] = floatx16{};
+    const uint32_t kl = lds0 + tr_lane_off<LK>(lane);                                           // K^T
+    const uint32_t sl = lds0 + (uint32_t)(Cfg::KB + Cfg::SB * 2 * wave) + tr_lane_off<4>(lane);  // dS'^T
 
-    // One 32-key sub-tile: two 16-key halves, NDT products each.  Element i
-    // of a transposed read (two ds_read_b64_tr_b16 of four rows each) holds
-    // row R0 + 8 (i / 4) + 4 hh + i % 4, for the K^T and the dS'^T operand
-    // alike.  PART: keys past S_kv (whose K rows read as zero) get a zero dS'
-    // as well.
-    auto sub = [&]<bool PART>(uint32_t so, int kv0, int g) {
+    // One key step: two 16-key halves.  Element i of a transposed read (two
+    // ds_read_b64_tr_b16 of four rows each) holds row R0 + 8 (i / 4) + 4 hh +
+    // i % 4, for the K^T and the dS'^T operand alike.  Keys past S_kv need no
+    // mask: their K rows read as zero and the dK/dV kernel stored a zero dS'
+    // for them.  A sub-tile that is not live (its queries all before the key
+    // group, or past S_q) takes a zero operand instead of its stale tile.
+    auto step_mfma = [&](uint32_t so, bool t0, bool t1) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int R0 = 32 * g + 16 * j;
-            half8 bs = ld_tr8(sl + so + 64u * R0, sl + so + 64u * (R0 + 8));
-            if constexpr (PART) {
-                const int lim = S_kv - (kv0 + R0 + 4 * hh);
+            const int R0 = 16 * j;
+            half8 bs[2];
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    if (8 * (i >> 2) + (i & 3) >= lim) bs[i] = (half_t)0.f;
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t a = sl + so + (uint32_t)(Cfg::SB * t);
+                bs[t] = ld_tr8(a + 64u * R0, a + 64u * (R0 + 8));
             }
+            if (!t0) bs[0] = half8{};
+            if (!t1) bs[1] = half8{};
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
                 const uint32_t a = (kl ^ (uint32_t)(64 * dt)) + so;
                 const half8 ak = ld_tr8(a + 16u * LK * R0, a + 16u * LK * (R0 + 8));
-                acc[dt] = mfma_f16(ak, bs, acc[dt]);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) acc[t][dt] = mfma_f16(ak, bs[t], acc[t][dt]);
             }
         }
     };
 
+    // Ring: the copies of step n + 2 go out once step n begins (their stage
+    // held step n - 1, which every wave has finished at that barrier); step
+    // n waits for its own copies with those of step n + 1 still in flight.
+    static_assert(NSTAGE == 3, "two steps of copies ahead");
+    int n_next = 0;  // copies of step n + 1 this wave issued
     if (nsteps > 0) issue(0);
+    if (nsteps > 1) n_next = issue(1);
     for (int step = 0; step < nsteps; ++step) {
-        wait_vm();
+        if (step + 1 < nsteps) wait_vm_upto(n_next);
+        else wait_vm();
         __syncthreads();
-        if (step + 1 < nsteps) issue(step + 1);
+        if (step + 2 < nsteps) n_next = issue(step + 2);
+        else n_next = 0;
         const int kv0 = step * BN;
-        const uint32_t so = (uint32_t)((step & 1) * Cfg::STAGE);
-        const bool part = kv0 + BN > S_kv;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            if (!sub_live(kv0, g)) continue;
-            if (part) sub.template operator()<true>(so, kv0, g);
-            else sub.template operator()<false>(so, kv0, g);
-        }
+        const bool t0 = sub_live(kv0, 0), t1 = sub_live(kv0, 1);
+        if (t0 || t1) step_mfma((uint32_t)((step % NSTAGE) * Cfg::STAGE), t0, t1);
     }
 
-    if (live && my_q < S_q) {
-        // dS' = dS (1-p) with dropout (keep_scale 1/(1-p)); every element
-        // dropped (keep_scale 0): dS' = dS
-        const float f = (p.c.use_dropout && p.c.keep_scale != 0.f) ? p.c.scale * p.c.keep_scale : p.c.scale;
-        half_t* dQb = static_cast<half_t*>(p.dq) + ((size_t)b * S_q + my_q) * D_qk;
-        if (D_qk == DQK) store_rows_f16<DQK>(dQb, acc, f, hh);
-        else store_rows_f16_n<DQK>(dQb, acc, f, hh, D_qk);
+    // dS' = dS (1-p) with dropout (keep_scale 1/(1-p)); every element
+    // dropped (keep_scale 0): dS' = dS
+    const float f = (p.c.use_dropout && p.c.keep_scale != 0.f) ? p.c.scale * p.c.keep_scale : p.c.scale;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int my_q = qw0 + 32 * t + pq;
+        if (my_q < S_q) {
+            half_t* dQb = static_cast<half_t*>(p.dq) + ((size_t)b * S_q + my_q) * D_qk;
+            if (D_qk == DQK) store_rows_f16<DQK>(dQb, acc[t], f, hh);
+            else store_rows_f16_n<DQK>(dQb, acc[t], f, hh, D_qk);
+        }
     }
 }
 
