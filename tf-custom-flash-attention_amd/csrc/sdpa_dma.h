@@ -394,6 +394,14 @@ __device__ __forceinline__ void dma16_at(rsrc_t r, uint32_t m0, uint32_t voff) {
                  : "s"(__builtin_amdgcn_readfirstlane((int)m0)), "v"(voff), "s"(r)
                  : "memory", "m0");
 }
+// The same with the non-temporal hint, for data read once (the stored dS of
+// the backward's dS path): L2 keeps the tiles that are read again.
+__device__ __forceinline__ void dma16_at_nt(rsrc_t r, uint32_t m0, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane((int)m0)), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Chunk swizzle of a tile that is only ever read transposed

@@ -442,8 +442,11 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
                 const int qb = (q_top - m * BQ) / BQ;
                 unsigned char* dst = static_cast<unsigned char*>(p.ds) + dsl.offset(b, kt, qb) + t * 8192 +
                                      (32 * kw + l32) * 64 + hh * 32;
-                *reinterpret_cast<half8*>(dst) = ds0;
-                *reinterpret_cast<half8*>(dst + 16) = ds1;
+                // non-temporal: the dS lines are not read again in this kernel, and
+                // left in L2 they evict the Q / dO tiles it re-reads (a step
+                // 2.766 -> 2.720 ms at c4; system-scope write-through: 3.2 ms)
+                __builtin_nontemporal_store(ds0, reinterpret_cast<half8*>(dst));
+                __builtin_nontemporal_store(ds1, reinterpret_cast<half8*>(dst + 16));
             }
 #pragma unroll
             for (int dt = 0; dt < DQK / 32; ++dt) {

@@ -108,7 +108,7 @@ void sdpa_bwd_dq_ds_f16_kernel(const BwdParams p, const int win) {
     const RowSrc ksrc = row_src(p.k, (size_t)b * S_kv, S_kv, D_qk * 2);
     TileCopy<BN, LK, NW, true> kc;
     kc.init(wave, lane, D_qk * 2, D_qk / 8);
-    TileCopy<BN, 4, 1, true> sc;  // 32 rows of 64 bytes: a plain 2 KB copy
+    TileCopy<BN, 4, 1, true> sc;  // lane offsets of a plain 2 KB copy (32 rows of 64 bytes)
     sc.init(0, lane, 64, 4);
     const uint32_t lds0 = lds_base();
     const int kv_end = CAUSAL ? min(S_kv, q0 + BM) : S_kv;
@@ -125,8 +125,11 @@ void sdpa_bwd_dq_ds_f16_kernel(const BwdParams p, const int win) {
             if (sub_live(kv0, t)) {
                 const unsigned char* src = dsb + dsl.offset(b, kv0 / DsLayout::KT, qb) + t * 8192 +
                                            (kv0 % DsLayout::KT) * 64;
-                sc.issue(RowSrc{uniform_ptr(src), BN, 64, 0x7FFFFFFF / 64},
-                         lds0 + so + (uint32_t)(Cfg::KB + Cfg::SB * (2 * wave + t)), 0);
+                // dS is read once: non-temporal (dQ 0.470 -> 0.425 ms at c4)
+                const rsrc_t rs = RowSrc{uniform_ptr(src), BN, 64, 0x7FFFFFFF / 64}.at(0);
+                const uint32_t m0 = lds0 + so + (uint32_t)(Cfg::KB + Cfg::SB * (2 * wave + t));
+#pragma unroll
+                for (int u = 0; u < decltype(sc)::count(0); ++u) dma16_at_nt(rs, m0 + 1024u * u, sc.voff + 1024u * u);
                 n += decltype(sc)::count(0);
             }
         }
