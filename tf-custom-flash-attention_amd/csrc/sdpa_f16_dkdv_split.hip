@@ -409,7 +409,8 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
             ds0 = half8_of(wd[0], wd[1], wd[2], wd[3]);
             ds1 = half8_of(wd[4], wd[5], wd[6], wd[7]);
         };
-        auto sub = [&](uint32_t qbase, int m, int t) {
+        // one sub-tile: dP, dS' (returned in d0 / d1 for the dS store) and dK
+        auto sub = [&](uint32_t qbase, int m, int t, half8& d0, half8& d1) {
             const uint32_t obase = qbase + Cfg::QB;
             const float* Fs = reinterpret_cast<const float*>(smem + obase + Cfg::OB);
             const uint32_t aO = obase + swO.row;
@@ -431,28 +432,32 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
             __builtin_amdgcn_sched_barrier(0);
             half8 ds0, ds1;
             elem(dpacc, de4, xv0, xv1, ds0, ds1);
-            if constexpr (DS) {
-                // dS' of this sub-tile into its chunk (DsLayout): this lane's
-                // key row, its 16 queries as the two halves of its 32 bytes;
-                // zero for keys past S_kv (the dQ kernel reads them unmasked)
-                if (kw0 + 31 >= S_kv && !key_ok) {
-                    ds0 = half8{};
-                    ds1 = half8{};
-                }
-                const int qb = (q_top - m * BQ) / BQ;
-                unsigned char* dst = static_cast<unsigned char*>(p.ds) + dsl.offset(b, kt, qb) + t * 8192 +
-                                     (32 * kw + l32) * 64 + hh * 32;
-                // non-temporal: the dS lines are not read again in this kernel, and
-                // left in L2 they evict the Q / dO tiles it re-reads (a step
-                // 2.766 -> 2.720 ms at c4; system-scope write-through: 3.2 ms)
-                __builtin_nontemporal_store(ds0, reinterpret_cast<half8*>(dst));
-                __builtin_nontemporal_store(ds1, reinterpret_cast<half8*>(dst + 16));
-            }
+            d0 = ds0;
+            d1 = ds1;
 #pragma unroll
             for (int dt = 0; dt < DQK / 32; ++dt) {
                 dkacc[dt] = mfma_f16(at[0][dt], ds0, dkacc[dt]);
                 dkacc[dt] = mfma_f16(at[1][dt], ds1, dkacc[dt]);
             }
+        };
+        // dS' of sub-tile t of block m into its chunk (DsLayout): this lane's key
+        // row, its 16 queries as the two halves of its 32 bytes; zero for keys
+        // past S_kv (the dQ kernel reads them unmasked).  Both sub-tiles' dS'
+        // go out at the end of the block, while the P role runs its dV
+        // products rather than its copies (issued beside those copies they
+        // cost c4's dK/dV 2.7% more), and non-temporal: the lines are not read
+        // again here, and left in L2 they evict the Q / dO tiles this kernel
+        // re-reads (a step 2.766 -> 2.720 ms; system-scope write-through 3.2 ms).
+        auto store_ds = [&](int m, int t, half8 d0, half8 d1) {
+            if (kw0 + 31 >= S_kv && !key_ok) {
+                d0 = half8{};
+                d1 = half8{};
+            }
+            const int qb = (q_top - m * BQ) / BQ;
+            unsigned char* dst = static_cast<unsigned char*>(p.ds) + dsl.offset(b, kt, qb) + t * 8192 +
+                                 (32 * kw + l32) * 64 + hh * 32;
+            __builtin_nontemporal_store(d0, reinterpret_cast<half8*>(dst));
+            __builtin_nontemporal_store(d1, reinterpret_cast<half8*>(dst + 16));
         };
         if constexpr (PCOPY) {
         // The P role copies every block and rewrites its delta row before the
@@ -465,8 +470,14 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
             const int m = n - 1;
             const int q0 = q_top - m * BQ;
             const uint32_t qbase = (uint32_t)((m % NSTAGE) * Cfg::STAGE);
-            if (sub_live(q0)) sub(qbase, m, 0);
-            if (sub_live(q0 + 32)) sub(qbase, m, 1);
+            half8 a0, a1, c0, c1;
+            const bool l0 = sub_live(q0), l1 = sub_live(q0 + 32);
+            if (l0) sub(qbase, m, 0, a0, a1);
+            if (l1) sub(qbase, m, 1, c0, c1);
+            if constexpr (DS) {
+                if (l0) store_ds(m, 0, a0, a1);
+                if (l1) store_ds(m, 1, c0, c1);
+            }
         }
         } else {
         for (int n = 0; n <= nsteps; ++n) {
@@ -495,9 +506,15 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
             const int m = n - 1;
             const int q0 = q_top - m * BQ;
             const uint32_t qbase = (uint32_t)((m % NSTAGE) * Cfg::STAGE);
-            if (sub_live(q0)) sub(qbase, m, 0);
+            half8 a0, a1, c0, c1;
+            const bool l0 = sub_live(q0), l1 = sub_live(q0 + 32);
+            if (l0) sub(qbase, m, 0, a0, a1);
             if (cp) od.issue(make_rsrc(dOb + (size_t)qn * D_v, (long long)(S_q - qn) * D_v * 2), stn + Cfg::QB, kw);
-            if (sub_live(q0 + 32)) sub(qbase, m, 1);
+            if (l1) sub(qbase, m, 1, c0, c1);
+            if constexpr (DS) {
+                if (l0) store_ds(m, 0, a0, a1);
+                if (l1) store_ds(m, 1, c0, c1);
+            }
         }
         }
         if (key_ok) {
