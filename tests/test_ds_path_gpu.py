@@ -179,7 +179,13 @@ def test_ds_stored_and_dq_product(pkg, O, shape):
     raw = ws[rows:].cpu().numpy().view(np.float16).astype(np.float64)
     idx, per_row = _ds_layout(S_q, S_kv, causal)
     assert raw.size == B * per_row * 8192
-    chunks = raw.reshape(B, per_row, 2, 128, 32)
+    # inside a 2 KB key group (1024 halves): position i of key r sits in
+    # plane p = 2 j + h (h = i >> 4, j = (i >> 3) & 1), row r ^ 4 p, half i & 7
+    r_, i_ = np.meshgrid(np.arange(32), np.arange(32), indexing="ij")
+    p_ = 2 * ((i_ >> 3) & 1) + (i_ >> 4)
+    gather = p_ * 256 + (r_ ^ (4 * p_)) * 8 + (i_ & 7)
+    assert sorted(gather.ravel()) == list(range(1024))
+    chunks = raw.reshape(B, per_row, 2, 4, 1024)[..., gather].reshape(B, per_row, 2, 128, 32)
     pi = _perm()
     # float64 reference dS = P (dP - delta), P gated at 1e-6
     f64 = lambda a: a.astype(np.float64)

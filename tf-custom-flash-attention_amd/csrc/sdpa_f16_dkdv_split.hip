@@ -440,9 +440,11 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
                 dkacc[dt] = mfma_f16(at[1][dt], ds1, dkacc[dt]);
             }
         };
-        // dS' of sub-tile t of block m into its chunk (DsLayout): this lane's key
-        // row, its 16 queries as the two halves of its 32 bytes; zero for keys
-        // past S_kv (the dQ kernel reads them unmasked).  Both sub-tiles' dS'
+        // dS' of sub-tile t of block m into its chunk (DsLayout): store j of
+        // this lane to slot(key, 2 j + h) of its key group, each store 1 KB in
+        // runs of four lanes (key rows of 64 bytes, one 16-byte piece per lane,
+        // made every lane a write request of its own); zero for keys past S_kv
+        // (the dQ kernel reads them unmasked).  Both sub-tiles' dS'
         // go out at the end of the block, while the P role runs its dV
         // products rather than its copies (issued beside those copies they
         // cost c4's dK/dV 2.7% more), and non-temporal: the lines are not read
@@ -455,9 +457,9 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
             }
             const int qb = (q_top - m * BQ) / BQ;
             unsigned char* dst = static_cast<unsigned char*>(p.ds) + dsl.offset(b, kt, qb) + t * 8192 +
-                                 (32 * kw + l32) * 64 + hh * 32;
-            __builtin_nontemporal_store(d0, reinterpret_cast<half8*>(dst));
-            __builtin_nontemporal_store(d1, reinterpret_cast<half8*>(dst + 16));
+                                 kw * 2048;
+            __builtin_nontemporal_store(d0, reinterpret_cast<half8*>(dst + DsLayout::slot(l32, hh)));
+            __builtin_nontemporal_store(d1, reinterpret_cast<half8*>(dst + DsLayout::slot(l32, 2 + hh)));
         };
         if constexpr (PCOPY) {
         // The P role copies every block and rewrites its delta row before the

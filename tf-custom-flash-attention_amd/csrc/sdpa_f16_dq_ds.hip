@@ -64,7 +64,8 @@ __global__ __launch_bounds__(256) void sdpa_bwd_rows_f16_kernel(const BwdParams 
 // the A operand K^T) and each wave's two dS' tiles, 32 keys x 32 queries as
 // stored (read transposed: the B operand dS'^T, lane = query).  The lanes of
 // a wave take the queries in the stored order (DsLayout), so the tiles are
-// copied as they lie; lane l32 owns queries qb 64 + 32 t + pi(l32).
+// copied as they lie (2 KB each, lane-contiguous); lane l32 owns queries
+// qb 64 + 32 t + pi(l32).
 // ---------------------------------------------------------------------------
 template <int DQK>
 struct DqDsCfg {
@@ -142,7 +143,19 @@ void sdpa_bwd_dq_ds_f16_kernel(const BwdParams p, const int win) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) acc[t][dt] = floatx16{};
     const uint32_t kl = lds0 + tr_lane_off<LK>(lane);                                           // K^T
-    const uint32_t sl = lds0 + (uint32_t)(Cfg::KB + Cfg::SB * 2 * wave) + tr_lane_off<4>(lane);  // dS'^T
+    // dS'^T: the transposed read of tr_lane_off<4> (row tr_row, 16-byte slot
+    // c: query positions 8 c + sub / 2 ..) at its place in the stored tile,
+    // slot(key, p) with p = 2 (c & 1) + (c >> 1); rows tr_row and tr_row + 8
+    // (slot(key + 16 n, p) = slot(key, p) + 256 n)
+    uint32_t sl0, sl8;
+    {
+        const int g16 = lane >> 4, i16 = lane & 15;
+        const int tr_row = 4 * (g16 >> 1) + (i16 >> 2), c = 2 * (g16 & 1) + ((i16 & 3) >> 1), sub = 8 * (i16 & 1);
+        const int pl = 2 * (c & 1) + (c >> 1);
+        const uint32_t base = lds0 + (uint32_t)(Cfg::KB + Cfg::SB * 2 * wave + sub);
+        sl0 = base + (uint32_t)DsLayout::slot(tr_row, pl);
+        sl8 = base + (uint32_t)DsLayout::slot(tr_row + 8, pl);
+    }
 
     // One key step: two 16-key halves.  Element i of a transposed read (two
     // ds_read_b64_tr_b16 of four rows each) holds row R0 + 8 (i / 4) + 4 hh +
@@ -157,8 +170,8 @@ void sdpa_bwd_dq_ds_f16_kernel(const BwdParams p, const int win) {
             half8 bs[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                const uint32_t a = sl + so + (uint32_t)(Cfg::SB * t);
-                bs[t] = ld_tr8(a + 64u * R0, a + 64u * (R0 + 8));
+                const uint32_t a = so + (uint32_t)(Cfg::SB * t) + 16u * R0;
+                bs[t] = ld_tr8(sl0 + a, sl8 + a);
             }
             if (!t0) bs[0] = half8{};
             if (!t1) bs[1] = half8{};

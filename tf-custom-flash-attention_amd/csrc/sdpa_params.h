@@ -61,9 +61,15 @@ struct BwdParams {
 // blocks (64 queries) qb >= qbb(kt) = min(128 kt, S_q) / 64, else all of
 // them.  Each visited (kt, qb) is a 16 KB chunk, and the chunks of a batch
 // row follow each other kt-major, qb-minor.  Inside a chunk: two 32-query
-// sub-tiles t, each [128 keys][32 queries] fp16 (64 bytes per key), the 32
-// queries in the order the dK/dV kernel's lanes hold them: position j is
-// query 8 ((j >> 2) & 3) + 4 (j >> 4) + (j & 3) of the sub-tile.
+// sub-tiles t of 8 KB, each four 2 KB key groups (32 keys), each four 512-byte
+// planes p of 32 slots of 16 bytes.  Slot slot(key, p) of plane p = 2 j + h
+// holds the key's dS' at query positions 16 h + 8 j .. + 7: one store j of the
+// dK/dV lane 32 h + key, so each store instruction writes 1 KB in whole 64-byte
+// runs of four lanes.  The key order inside a plane (key ^ 4 p) puts the four
+// planes' rows 0-3 in different LDS banks, for the dQ kernel's transposed read
+// of the group copied as it lies.  The 32 query positions are in the order the
+// dK/dV kernel's lanes hold them: position i is query
+// 8 ((i >> 2) & 3) + 4 (i >> 4) + (i & 3) of the sub-tile.
 struct DsLayout {
     static constexpr int KT = 128, QBK = 64, CHUNK = 16384;
     int S_q, QB, F, tiles;
@@ -84,6 +90,8 @@ struct DsLayout {
         return ((size_t)b * (size_t)per_row() + (size_t)prefix(kt) + (size_t)(qb - qbb(kt))) * CHUNK;
     }
     __host__ __device__ size_t bytes(int B) const { return (size_t)B * (size_t)per_row() * CHUNK; }
+    // byte offset of (key, plane p) inside its 2 KB key group
+    __host__ __device__ static constexpr int slot(int key, int p) { return p * 512 + (key ^ (4 * p)) * 16; }
 };
 
 }  // namespace sdpa
