@@ -29,22 +29,44 @@ namespace {
 // Row values.  One lane pair per query row (lane = row, hh = half of the
 // features): delta = sum_d dO O in the order of the dQ kernel's prologue, and
 // stats2 = stats log2(e) + kGateShift as one fma, so that both paths hand the
-// dK/dV kernel the same values.
+// dK/dV kernel the same values.  The 128 rows of dO and O a workgroup covers
+// are first copied into LDS whole (each copy 1 KB of consecutive bytes; a
+// lane's own 16-byte pieces, 32 rows apart per load, made every lane a
+// request of its own) and read back per lane in the swizzled row layout.
 // ---------------------------------------------------------------------------
 template <int DV>
+struct RowsCfg {
+    static constexpr int NW = 4, NT = 64 * NW, ROWS = 32 * NW, L = DV / 8;
+    static constexpr int TB = ROWS * L * 16;  // one tile (dO or O)
+    static constexpr size_t LDS_BYTES = 2 * (size_t)TB;
+};
+
+template <int DV>
 __global__ __launch_bounds__(256) void sdpa_bwd_rows_f16_kernel(const BwdParams p) {
-    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5, wave = tid >> 6;
+    using Cfg = RowsCfg<DV>;
+    constexpr int L = Cfg::L, ROWS = Cfg::ROWS, NW = Cfg::NW, TB = Cfg::TB;
+    const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int S_q = p.s.S_q, D_v = p.s.D_v;
-    const int tiles = (S_q + 127) / 128;
+    const int tiles = (S_q + ROWS - 1) / ROWS;
     const int b = (int)(blockIdx.x / (unsigned)tiles), qt = (int)(blockIdx.x % (unsigned)tiles);
-    const int my_q = qt * 128 + 32 * wave + l32;
-    const half_t* Ob = static_cast<const half_t*>(p.o) + (size_t)b * S_q * D_v;
-    const half_t* dOb = static_cast<const half_t*>(p.d_o) + (size_t)b * S_q * D_v;
+    const int q0 = qt * ROWS, my_q = q0 + 32 * wave + l32;
+    const size_t row0 = (size_t)b * S_q + q0;
+    // rows past S_q and features past D_v read as zero
+    TileCopy<ROWS, L, NW> tc;
+    tc.init(wave, lane, D_v * 2, D_v / 8);
+    const uint32_t m0 = lds_base() + 1024u * (uint32_t)wave;
+    tc.issue(row_src(p.d_o, row0, S_q - q0, D_v * 2), m0, wave);
+    tc.issue(row_src(p.o, row0, S_q - q0, D_v * 2), m0 + (uint32_t)TB, wave);
+    wait_vm();
+    __syncthreads();
+    SwzLane<L> sw;
+    sw.init(lane);
     float dpart = 0.f;
 #pragma unroll
     for (int ks = 0; ks < DV / 16; ++ks) {
-        const half8 d8 = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(dOb, my_q, S_q, 16 * ks + 8 * hh, D_v, D_v));
-        const half8 o8 = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Ob, my_q, S_q, 16 * ks + 8 * hh, D_v, D_v));
+        const half8 d8 = lds_row<L>(sw.row, ks, 32 * wave);
+        const half8 o8 = lds_row<L>(TB + sw.row, ks, 32 * wave);
 #pragma unroll
         for (int e = 0; e < 8; ++e) dpart += (float)d8[e] * (float)o8[e];
     }
@@ -226,7 +248,8 @@ hipError_t launch_bwd_rows_f16(const BwdParams& p, hipStream_t stream) {
     if (n > 0x7FFFFFFFLL) return hipErrorInvalidValue;
     return with_dim(p.s.D_v, [&](auto dv) {
         constexpr int DV = decltype(dv)::value;
-        return launch_kernel<sdpa_bwd_rows_f16_kernel<DV>>((unsigned)n, 256, 0, stream, p);
+        using Cfg = RowsCfg<DV>;
+        return launch_kernel<sdpa_bwd_rows_f16_kernel<DV>>((unsigned)n, Cfg::NT, Cfg::LDS_BYTES, stream, p);
     });
 }
 
