@@ -36,6 +36,9 @@ CASES = [
     Cfg("ds_cross_d80_31x1000", "f16", 1, 31, 1000, 80, 80, False, 0.1, 80 ** -0.5, 11, 3),
     Cfg("ds_causal_d128_drop_all", "f16", 2, 160, 160, 128, 128, True, 1.5, 128 ** -0.5, 2, 6),
     Cfg("ds_causal_d128_one_row", "f16", 2, 1, 1, 128, 128, True, 0.0, 128 ** -0.5, 0, 0),
+    # feature sizes that end inside a pair of 16-byte chunks (the row kernel's
+    # lanes read chunks 2 ks + h: chunk 9 of D_v = 72 reads as zero)
+    Cfg("ds_causal_120x72", "f16", 2, 257, 257, 120, 72, True, 0.1, 120 ** -0.5, 4, 5),
 ]
 
 
