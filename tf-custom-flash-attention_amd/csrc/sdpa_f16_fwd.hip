@@ -318,11 +318,15 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
     // Step `step`: wait for its block (the copies of the NSTAGE - 2 later
     // blocks may still fly; all of them at the tail), synchronise, multiply,
     // and copy block step + NSTAGE - 1 into the slot of block step - 1 (every
-    // wave has finished reading it).  The waves of a workgroup issue their
-    // copies at different points of the step (wave w after region w: at once,
-    // after R1, after R2, after R3): issued together, right after the
-    // barrier, they queue behind each other in the CU's address unit and
-    // stall all four waves at the same time.
+    // wave has finished reading it).  Waves 0 and 1 issue their copies right
+    // after the barrier, waves 2 and 3 after R1.  Issued by all four there,
+    // they queue behind each other in the CU's address unit and stall all
+    // four waves at once; spread over four points (the barrier, after R1, R2
+    // and R3), the last wave's copies had only R4 to land before the next
+    // step waits for them.  Only the copy point after R1 stays in the step's
+    // code: a copy branch at the end of R2 or R3 also splits the compiler's
+    // scheduling regions there (with them compiled in but never taken, c4's
+    // forward took 0.717 against 0.695 ms; with four points, 0.711 ms).
     const bool live = qw0 < S_q;
     auto do_step = [&]<bool PART>(int step) {
         const uint32_t so = (uint32_t)((step % NSTAGE) * Cfg::STAGE);
@@ -330,16 +334,17 @@ void sdpa_fwd_f16_dma_kernel(const FwdParams p, const int win) {
         else wait_vm();
         __syncthreads();
         const bool cp = step + NSTAGE - 1 < nsteps;
-        static_assert(NW == 4, "one copy point per wave");
-        if (cp && wave == 0) issue(step + NSTAGE - 1);
+        static_assert(NW == 4, "copy points of four waves");
+        const bool late = wave >= 2;  // issues after R1
+        if (cp && !late) issue(step + NSTAGE - 1);
         const int kv0 = step * BN;
         auto mid = [&](int k) {
-            if (cp && wave == k) issue(step + NSTAGE - 1);
+            if (k == 1 && cp && late) issue(step + NSTAGE - 1);
         };
         if (!PART || (live && !(CAUSAL && kv0 > qw0 + 31))) {  // else: no visible key in this step
             fwd_step.template operator()<PART>(kv0, so, mid);
         }
-        else if (cp && wave != 0)
+        else if (cp && late)
             issue(step + NSTAGE - 1);
         if constexpr (DROP) st_blk += (uint64_t)BN * kLcgMul;
     };
