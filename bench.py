@@ -275,12 +275,14 @@ def main():
     achieved = kflops[dom] / (per[dom] * 1e-3) / 1e12
     # fp16 shapes with D % 8 == 0 run the DMA-fed kernels (sdpa_f16_fwd/dq/dkdv.hip)
     sfx = "f16_dma" if (dt == "f16" and D_qk % 8 == 0 and D_v % 8 == 0) else dt
-    # (dK/dV of a feature width above 64 runs the split-role variant)
-    kv_sfx = "f16_split" if (sfx == "f16_dma" and max(D_qk, D_v) > 64) else sfx
-    dq_sym = "sdpa_bwd_dq_ds_f16_kernel" if use_ds else "sdpa_bwd_dq_%s_kernel" % sfx
+    # (dK/dV of a feature width above 64 runs the split-role variant, fp16
+    # with the DMA-fed kernels and fp32 alike)
+    split = max(D_qk, D_v) > 64 and (sfx == "f16_dma" or dt == "f32")
+    kv_sfx = ("f16_split" if dt == "f16" else "f32_split") if split else sfx
+    dq_sym = "sdpa_bwd_dq_ds_%s_kernel" % dt if use_ds else "sdpa_bwd_dq_%s_kernel" % sfx
     kernel_symbol = {"sdpa_fwd": "sdpa_fwd_%s_kernel" % sfx, "sdpa_bwd_dq": dq_sym,
                      "sdpa_bwd_dkdv": "sdpa_bwd_dkdv_%s_kernel" % kv_sfx,
-                     "sdpa_bwd_rows": "sdpa_bwd_rows_f16_kernel"}[dom]
+                     "sdpa_bwd_rows": "sdpa_bwd_rows_%s_kernel" % dt}[dom]
 
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * (1 << 20)

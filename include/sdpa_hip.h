@@ -139,11 +139,11 @@ int sdpa_hip_bwd_dkdv(int dtype, const void* q, const void* k, const void* v, co
 
 /* ---- backward, dS path --------------------------------------------------
  * No counterpart in the reference (an MI355X choice of how its two backward
- * kernels divide the work).  For float16 with a feature size over 64, the
- * dK/dV kernel can store the dS it forms (fp16, every visited score: about
- * B * S_q * S_kv bytes under the causal mask, twice that without) and dQ is
- * then one product with it, instead of a kernel that forms S, P, dP and dS
- * again.  sdpa_hip_bwd takes this path whenever the shape qualifies, the
+ * kernels divide the work).  For float16 and float32 with a feature size
+ * over 64, the dK/dV kernel can store the dS it forms (in T, every visited
+ * score: about B * S_q * S_kv * sizeof(T) / 2 bytes under the causal mask,
+ * twice that without) and dQ is then one product with it, instead of a
+ * kernel that forms S, P, dP and dS again.  sdpa_hip_bwd takes this path whenever the shape qualifies, the
  * tensors are 16-byte aligned and workspace_bytes is at least
  * sdpa_hip_bwd_workspace_bytes_ds(...); with a smaller workspace (at least
  * sdpa_hip_bwd_workspace_bytes(B, S_q)) it takes the other one.  For shapes

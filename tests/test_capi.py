@@ -159,21 +159,24 @@ def test_launch_entry_points_reject_before_device_work(pkg):
     assert L.sdpa_hip_bwd_workspace_bytes(0, 4096) == 0
 
 
-def _ds_chunks(S_q, S_kv, causal):
-    """Query blocks (64 rows) the split dK/dV kernel visits, summed over its
-    key tiles (128 keys): the dS chunks of one batch row, counted the way the
-    kernel walks them (q_begin, nsteps of sdpa_f16_dkdv_split.hip)."""
+def _ds_chunks(S_q, S_kv, causal, qbk=64):
+    """Query blocks (qbk rows: 64 in the fp16 split dK/dV kernel, 32 in the
+    fp32 one) the kernel visits, summed over its key tiles (128 keys): the dS
+    chunks of one batch row, counted the way the kernels walk them (q_begin
+    and the block count of sdpa_f16_dkdv_split.hip and of
+    sdpa_bwd_dkdv_f32_split_kernel)."""
     n = 0
     for kt in range((S_kv + 127) // 128):
-        q_begin = (min(128 * kt, S_q) // 64) * 64 if causal else 0
-        n += (S_q - q_begin + 63) // 64
+        q_begin = (min(128 * kt, S_q) // qbk) * qbk if causal else 0
+        n += (S_q - q_begin + qbk - 1) // qbk
     return n
 
 
 def test_ds_workspace_bytes(pkg):
     """sdpa_hip_bwd_workspace_bytes_ds = the per-row workspace + 16 KB per
-    visited (key tile, query block) per batch row, for float16 with a feature
-    size over 64; the per-row size for every other shape."""
+    visited (key tile, query block) per batch row, for float16 (query blocks
+    of 64) and float32 (blocks of 32) with a feature size over 64; the
+    per-row size for every other shape."""
     L = pkg.library()
     for B, S_q, S_kv, D_qk, D_v, causal in [(128, 4096, 4096, 128, 128, 1), (3, 333, 333, 128, 128, 1),
                                              (2, 130, 300, 128, 64, 0), (2, 300, 100, 64, 128, 0),
@@ -182,11 +185,15 @@ def test_ds_workspace_bytes(pkg):
         rows = L.sdpa_hip_bwd_workspace_bytes(B, S_q)
         want = rows + B * _ds_chunks(S_q, S_kv, causal) * 16384
         assert L.sdpa_hip_bwd_workspace_bytes_ds(1, B, S_q, S_kv, D_qk, D_v, causal) == want
-        # fp32, or both sides <= 64: the per-row workspace only
-        assert L.sdpa_hip_bwd_workspace_bytes_ds(0, B, S_q, S_kv, D_qk, D_v, causal) == rows
+        want32 = rows + B * _ds_chunks(S_q, S_kv, causal, 32) * 16384
+        assert L.sdpa_hip_bwd_workspace_bytes_ds(0, B, S_q, S_kv, D_qk, D_v, causal) == want32
+        # both sides <= 64: the per-row workspace only
         assert L.sdpa_hip_bwd_workspace_bytes_ds(1, B, S_q, S_kv, 64, 64, causal) == rows
+        assert L.sdpa_hip_bwd_workspace_bytes_ds(0, B, S_q, S_kv, 64, 64, causal) == rows
     # c4: 1056 chunks per batch row under the causal mask (half of 32 x 64, plus the diagonal)
     assert _ds_chunks(4096, 4096, True) == 1056
+    # c5 in fp32: 128 key tiles x 16 query blocks per batch row (2 GiB at B = 64)
+    assert _ds_chunks(512, 16384, False, 32) == 2048
     assert L.sdpa_hip_bwd_workspace_bytes_ds(1, 0, 4096, 4096, 128, 128, 1) == 0
     assert L.sdpa_hip_bwd_workspace_bytes_ds(1, 2, 64, 0, 128, 128, 0) == L.sdpa_hip_bwd_workspace_bytes(2, 64)
 
@@ -202,8 +209,10 @@ def test_ds_phase_rejects_before_device_work(pkg):
     def phase(ph, dtype, D_qk=128, D_v=128, ws=big, B=2):
         return L.sdpa_hip_bwd_ds_phase(ph, dtype, *([fake] * 10), ws, B, 64, 64, D_qk, D_v, 1.0, 0.0, 1, 0, 0,
                                        None)
-    assert phase(0, 0) == pkg.SDPA_ERR_DS_PATH                 # fp32
     assert phase(1, 1, 64, 64) == pkg.SDPA_ERR_DS_PATH         # both sides <= 64
+    assert phase(0, 0, 64, 64) == pkg.SDPA_ERR_DS_PATH         # fp32, both sides <= 64
+    small32 = L.sdpa_hip_bwd_workspace_bytes_ds(0, 2, 64, 64, 128, 128, 1) - 1
+    assert phase(1, 0, ws=small32) == pkg.SDPA_ERR_DS_PATH     # fp32 workspace one byte short
     assert phase(3, 1) == pkg.SDPA_ERR_DS_PATH                 # no such phase
     assert phase(-1, 1) == pkg.SDPA_ERR_DS_PATH
     small = L.sdpa_hip_bwd_workspace_bytes_ds(1, 2, 64, 64, 128, 128, 1) - 1

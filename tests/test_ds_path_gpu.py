@@ -1,6 +1,7 @@
-"""The dS path of the fp16 backward: with the workspace of
+"""The dS path of the backward: with the workspace of
 sdpa_hip_bwd_workspace_bytes_ds, the dK/dV kernel stores the dS it forms and
-dQ is one product with it (sdpa_f16_dq_ds.hip).
+dQ is one product with it (sdpa_f16_dq_ds.hip for fp16, sdpa_f32_dq_ds.hip
+for fp32).
 
 Every case is checked three ways:
   - against the oracle, at north_star's fp16 tolerances (run_and_check, which
@@ -8,7 +9,8 @@ Every case is checked three ways:
   - against the path that forms dS in both kernels (the per-row workspace
     only): dK and dV bit-identical (same dK/dV kernel, and the row kernel
     hands it the values the other path's dQ kernel computes), dQ within the
-    rounding of P to fp16 before dS is formed;
+    rounding of P to fp16 before dS is formed (fp16), or of the other path's
+    own summation order for S and dP (fp32);
   - the three launches as separate calls (sdpa_hip_bwd_ds_phase) against the
     single call, bit-identical.
 Shapes cover several key tiles, ragged query and key lengths (the last query
@@ -39,7 +41,21 @@ CASES = [
     # feature sizes that end inside a pair of 16-byte chunks (the row kernel's
     # lanes read chunks 2 ks + h: chunk 9 of D_v = 72 reads as zero)
     Cfg("ds_causal_120x72", "f16", 2, 257, 257, 120, 72, True, 0.1, 120 ** -0.5, 4, 5),
+    # fp32 (the split dK/dV kernel's query blocks of 32)
+    Cfg("ds32_causal_d128_p0.1", "f32", 2, 300, 300, 128, 128, True, 0.1, 128 ** -0.5, 5, 9),
+    Cfg("ds32_cross_128x64", "f32", 2, 100, 1000, 128, 64, False, 0.0, 128 ** -0.5, 3, 4),
+    Cfg("ds32_cross_64x128_p0.2", "f32", 2, 257, 130, 64, 128, False, 0.2, 64 ** -0.5, 1, 2),
+    Cfg("ds32_causal_100x36", "f32", 2, 161, 161, 100, 36, True, 0.05, 100 ** -0.5, 7, 8),
+    Cfg("ds32_causal_drop_all", "f32", 2, 96, 96, 128, 128, True, 1.5, 128 ** -0.5, 2, 6),
 ]
+
+
+def _dcode(c):
+    return 1 if c.dtype == "f16" else 0
+
+
+def _bits(a):
+    return a.view(np.uint16 if a.dtype == np.float16 else np.uint32)
 
 
 def _grads(pkg, c, q, k, v, o, s, d_o, ds_path):
@@ -53,12 +69,12 @@ def _phases(pkg, c, q, k, v, o, s, d_o):
     L = pkg.library()
     B, S_q, D_qk = q.shape
     S_kv, D_v = k.shape[1], v.shape[2]
-    ws_bytes = int(L.sdpa_hip_bwd_workspace_bytes_ds(1, B, S_q, S_kv, D_qk, D_v, int(c.causal)))
+    ws_bytes = int(L.sdpa_hip_bwd_workspace_bytes_ds(_dcode(c), B, S_q, S_kv, D_qk, D_v, int(c.causal)))
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=q.device)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     h = torch.cuda.current_stream().cuda_stream
     for phase in range(3):
-        rc = L.sdpa_hip_bwd_ds_phase(phase, 1, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+        rc = L.sdpa_hip_bwd_ds_phase(phase, _dcode(c), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                                      s.data_ptr(), d_o.data_ptr(), dq.data_ptr(), dk.data_ptr(),
                                      dv.data_ptr(), ws.data_ptr(), ws_bytes, B, S_q, S_kv, D_qk, D_v,
                                      float(c.scale), float(c.dropout), int(c.causal), c.seed, c.offset, h)
@@ -71,7 +87,7 @@ def _phases(pkg, c, q, k, v, o, s, d_o):
 def test_ds_path(pkg, O, c):
     L = pkg.library()
     rows = int(L.sdpa_hip_bwd_workspace_bytes(c.B, c.S_q))
-    full = int(L.sdpa_hip_bwd_workspace_bytes_ds(1, c.B, c.S_q, c.S_kv, c.D_qk, c.D_v, int(c.causal)))
+    full = int(L.sdpa_hip_bwd_workspace_bytes_ds(_dcode(c), c.B, c.S_q, c.S_kv, c.D_qk, c.D_v, int(c.causal)))
     assert full > rows  # the shape takes the dS path
     run_and_check(pkg, O, c, fp32_sum_allowance=True)
 
@@ -86,14 +102,15 @@ def test_ds_path(pkg, O, c):
     f = lambda a: a.astype(np.float32)
     ddq = float(np.abs(f(dq_a) - f(dq_b)).max()) if dq_a.size else 0.0
     print(f"[ds] {c.name}: dq ds-path vs recompute max|diff|={ddq:.3e}", flush=True)
-    assert np.array_equal(dk_a.view(np.uint16), dk_b.view(np.uint16))
-    assert np.array_equal(dv_a.view(np.uint16), dv_b.view(np.uint16))
-    # the recompute path forms dS from fp32 P, the dS path from its fp16 copy:
-    # a relative 2^-11 on each term before dS is rounded to fp16 itself
+    assert np.array_equal(_bits(dk_a), _bits(dk_b))
+    assert np.array_equal(_bits(dv_a), _bits(dv_b))
+    # fp16: the recompute path forms dS from fp32 P, the dS path from its fp16
+    # copy: a relative 2^-11 on each term before dS is rounded to fp16 itself.
+    # fp32: the same dS up to the two kernels' summation orders for S and dP.
     scale_g = max(1.0, float(np.abs(f(dq_b)).max()) if dq_b.size else 1.0)
-    assert ddq <= 4e-3 * scale_g
+    assert ddq <= (4e-3 if c.dtype == "f16" else 2e-5) * scale_g
     for a, b in ((dq_a, dq_p), (dk_a, dk_p), (dv_a, dv_p)):
-        assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+        assert np.array_equal(_bits(a), _bits(b))
 
 
 def test_ds_path_workspace_selects_path(pkg, O):
@@ -229,3 +246,87 @@ def test_ds_stored_and_dq_product(pkg, O, shape):
           f"dQ vs scale*dS_stored*K max|err|={err_dq:.3e}", flush=True)
     assert err_ds <= 2e-3 * max(1.0, ref_ds)
     assert err_dq <= 2e-3 * max(1.0, float(np.abs(dq_host).max()))
+
+
+def _ds_layout32(S_q, S_kv, causal):
+    """(kt, qb) -> chunk index within a batch row, and chunks per row, for the
+    fp32 split dK/dV kernel: key tiles of 128, query blocks of 32 (its
+    q_begin), kt-major."""
+    idx, n = {}, 0
+    for kt in range((S_kv + 127) // 128):
+        q_begin = (min(128 * kt, S_q) // 32) * 32 if causal else 0
+        for qb in range(q_begin // 32, (S_q + 31) // 32):
+            idx[(kt, qb)] = n
+            n += 1
+    return idx, n
+
+
+@pytest.mark.parametrize("shape", [(1, 200, 200, 128, 128, True), (2, 100, 260, 128, 64, False),
+                                   (1, 70, 70, 100, 36, True)],
+                         ids=["f32_causal_d128_S200", "f32_cross_128x64", "f32_causal_100x36"])
+def test_ds32_stored_and_dq_product(pkg, O, shape):
+    """fp32: the stored dS against a float64 dS of the same inputs at every
+    stored position (key rows of 32 floats, a lane's 16 values at query
+    positions 16 h + r), and phase 2's dQ against scale * (stored dS) K."""
+    B, S_q, S_kv, D_qk, D_v, causal = shape
+    c = Cfg("ds32_diag", "f32", B, S_q, S_kv, D_qk, D_v, causal, 0.0, D_qk ** -0.5, 4, 1)
+    from _common import make_inputs
+    qn, kn, vn, don = make_inputs(c)
+    q, k, v, d_o = _t(qn), _t(kn), _t(vn), _t(don)
+    o, s = pkg.sdpa(q, k, v, 4, 1, dropout=0.0, scale=c.scale, causal_mask=causal)
+    L = pkg.library()
+    rows = int(L.sdpa_hip_bwd_workspace_bytes(B, S_q))
+    full = int(L.sdpa_hip_bwd_workspace_bytes_ds(0, B, S_q, S_kv, D_qk, D_v, int(causal)))
+    ws = torch.zeros((full,), dtype=torch.uint8, device=q.device)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    h = torch.cuda.current_stream().cuda_stream
+    for phase in range(3):
+        rc = L.sdpa_hip_bwd_ds_phase(phase, 0, q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                     s.data_ptr(), d_o.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                     ws.data_ptr(), full, B, S_q, S_kv, D_qk, D_v, float(c.scale), 0.0,
+                                     int(causal), 4, 1, h)
+        assert rc == 0
+    torch.cuda.synchronize()
+    raw = ws[rows:].cpu().numpy().view(np.float32).astype(np.float64)
+    idx, per_row = _ds_layout32(S_q, S_kv, causal)
+    assert raw.size == B * per_row * 4096
+    chunks = raw.reshape(B, per_row, 128, 32)  # [chunk][key][position]
+    pi = _perm()
+    f64 = lambda a: a.astype(np.float64)
+    o_h, s_h = f64(_np(o)), f64(_np(s))
+    S = c.scale * np.einsum("bid,bjd->bij", f64(qn), f64(kn))
+    P = np.exp(S - s_h[..., None])
+    if causal:
+        P = np.where(np.tril(np.ones((S_q, S_kv), bool))[None], P, 0.0)
+    P = np.where(P > 1e-6, P, 0.0)
+    dP = np.einsum("bid,bjd->bij", f64(don), f64(vn))
+    delta = np.einsum("bid,bid->bi", f64(don), o_h)
+    dS = P * (dP - delta[..., None])
+    stored = np.zeros((B, S_q, S_kv))
+    seen = np.zeros((B, S_q, S_kv), bool)
+    for (kt, qb), ci in idx.items():
+        q_idx = qb * 32 + pi
+        for kw in range(4):
+            kw0 = 128 * kt + 32 * kw
+            q0 = 32 * qb
+            if not (kw0 < S_kv and q0 < S_q and not (causal and q0 + 31 < kw0)):
+                continue
+            blk = chunks[:, ci, 32 * kw:32 * kw + 32, :]  # [B, key, position]
+            for kk in range(32):
+                key = kw0 + kk
+                if key >= S_kv:
+                    assert not blk[:, kk, :].any(), "keys past S_kv are stored as zero"
+                    continue
+                ok = q_idx < S_q
+                stored[:, q_idx[ok], key] = blk[:, kk, ok]
+                seen[:, q_idx[ok], key] = True
+    need = np.abs(dS) > 0
+    assert seen[need].all(), "a nonzero dS was not stored"
+    err_ds = float(np.abs(stored - dS)[seen].max())
+    ref_ds = float(np.abs(dS).max())
+    dq_host = c.scale * np.einsum("bij,bjd->bid", stored, f64(kn))
+    err_dq = float(np.abs(f64(_np(dq)) - dq_host).max())
+    print(f"[ds32] {shape}: stored dS max|err|={err_ds:.3e} (max|dS|={ref_ds:.3e}); "
+          f"dQ vs scale*dS_stored*K max|err|={err_dq:.3e}", flush=True)
+    assert err_ds <= 1e-5 * max(1.0, ref_ds)
+    assert err_dq <= 1e-5 * max(1.0, float(np.abs(dq_host).max()))

@@ -201,8 +201,8 @@ def sdpa_grad(q, k, v, o, stats, d_o, seed=0, offset=0, dropout: float = 0.0,
     """Gradient op ``SdpaGrad`` (sdpa_ops.cc:34-63): returns ``(dq, dk, dv)``.
 
     ``ds_path``: give the backward the workspace of its dS path
-    (``sdpa_hip_bwd_workspace_bytes_ds``: float16 with a feature size over
-    64 then stores dS in the dK/dV kernel and forms dQ from it); False gives
+    (``sdpa_hip_bwd_workspace_bytes_ds``: float16 or float32 with a feature
+    size over 64 then stores dS in the dK/dV kernel and forms dQ from it); False gives
     it the per-row workspace only, and both kernels form dS."""
     import torch
     check_bwd(q, k, v, o, stats, d_o, seed, offset, causal_mask)

@@ -884,7 +884,7 @@ struct BwdKVF32SplitCfg {
     static_assert(LDS_BYTES <= 160 * 1024, "one workgroup per CU");
 };
 
-template <int DQK, int DV, bool VEC, bool DROP>
+template <int DQK, int DV, bool VEC, bool DROP, bool DS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_bwd_dkdv_f32_split_kernel(const BwdParams p) {
     using Cfg = BwdKVF32SplitCfg<DQK, DV>;
@@ -1048,6 +1048,11 @@ void sdpa_bwd_dkdv_f32_split_kernel(const BwdParams p) {
         floatx16 dkacc[DQK / 32];
 #pragma unroll
         for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};
+        // dS path: this key group's dS of each visited block goes to its
+        // chunk (DsLayout32), the lane's 16 values at query positions
+        // 16 hh + r of its key row; zero for keys past S_kv (the dQ kernel
+        // reads them unmasked)
+        const DsLayout32 dsl(S_q, S_kv, causal);
 
         for (int n = 0; n <= nblk; ++n) {
             __syncthreads();
@@ -1082,6 +1087,17 @@ void sdpa_bwd_dkdv_f32_split_kernel(const BwdParams p) {
                             p0 = __builtin_fabsf(xv[e]);
                         }
                         dpacc[r] = p0 * (dpk - de4[e]);
+                    }
+                }
+                if constexpr (DS) {
+                    float* dst = reinterpret_cast<float*>(static_cast<unsigned char*>(p.ds) +
+                                                          dsl.offset(b, kt, q0 / BQ) + kw * 4096 + l32 * 128 + hh * 64);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        floatx4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = key_ok ? dpacc[4 * u + e] : 0.f;
+                        __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst + 4 * u));
                     }
                 }
 #pragma unroll
@@ -1149,10 +1165,18 @@ hipError_t launch_bwd(const BwdParams& p, DType dtype, bool vec, int phases, hip
                         if (phases & kBwdDq)
                             err = launch_kernel<sdpa_bwd_dq_f32_kernel<DQK, DV, V, D>>(gq, CQ::NT, CQ::LDS_BYTES, stream, p);
                         if (err == hipSuccess && (phases & kBwdDkDv)) {
-                            if constexpr (SDPA_F32_SPLIT && (DQK == 128 || DV == 128))
-                                err = launch_kernel<sdpa_bwd_dkdv_f32_split_kernel<DQK, DV, V, D>>(
-                                    (unsigned)(((S_kv + CS::BKV - 1) / CS::BKV) * B), CS::NT, CS::LDS_BYTES, stream, p);
-                            else
+                            if constexpr (SDPA_F32_SPLIT && (DQK == 128 || DV == 128)) {
+                                static_assert(CS::BKV == DsLayout32::KT && CS::BQ == DsLayout32::QBK, "dS chunk geometry");
+                                const unsigned gs = (unsigned)(((S_kv + CS::BKV - 1) / CS::BKV) * B);
+                                if (p.ds)
+                                    err = launch_kernel<sdpa_bwd_dkdv_f32_split_kernel<DQK, DV, V, D, true>>(
+                                        gs, CS::NT, CS::LDS_BYTES, stream, p);
+                                else
+                                    err = launch_kernel<sdpa_bwd_dkdv_f32_split_kernel<DQK, DV, V, D, false>>(
+                                        gs, CS::NT, CS::LDS_BYTES, stream, p);
+                            } else if (p.ds) {
+                                err = hipErrorInvalidValue;  // the dS path needs the split kernel
+                            } else
                                 err = launch_kernel<sdpa_bwd_dkdv_f32_kernel<DQK, DV, V, D>>(gk, CK::NT, CK::LDS_BYTES, stream, p);
                         }
                     }

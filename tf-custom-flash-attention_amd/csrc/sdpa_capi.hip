@@ -153,10 +153,11 @@ size_t sdpa_hip_bwd_workspace_bytes(int B, int S_q) {
 }  // extern "C"
 
 namespace {
-// The dS path's shapes: fp16 through the split dK/dV kernel, nothing empty.
+// The dS path's shapes: fp16 or fp32 through a split dK/dV kernel, nothing
+// empty.
 bool ds_shape(int dtype, int B, int S_q, int S_kv, int D_qk, int D_v) {
-    return dtype == SDPA_DTYPE_F16 && B > 0 && S_q > 0 && S_kv > 0 && D_qk > 0 && D_v > 0 &&
-           sdpa::bwd_ds_shape(D_qk, D_v);
+    return (dtype == SDPA_DTYPE_F16 || dtype == SDPA_DTYPE_F32) && B > 0 && S_q > 0 && S_kv > 0 && D_qk > 0 &&
+           D_v > 0 && sdpa::bwd_ds_shape(D_qk, D_v);
 }
 }  // namespace
 
@@ -167,6 +168,7 @@ size_t sdpa_hip_bwd_workspace_bytes_ds(int dtype, int B, int S_q, int S_kv, int 
     const size_t rows = sdpa_hip_bwd_workspace_bytes(B, S_q);
     if (!ds_shape(dtype, B, S_q, S_kv, D_qk, D_v) || D_qk > 128 || D_v > 128) return rows;
     // the row values first (a multiple of 256 bytes), the stored dS after them
+    if (dtype == SDPA_DTYPE_F32) return rows + sdpa::DsLayout32(S_q, S_kv, causal_mask != 0).bytes(B);
     return rows + sdpa::DsLayout(S_q, S_kv, causal_mask != 0).bytes(B);
 }
 
@@ -231,9 +233,14 @@ int bwd_entry(Mode mode, int phases, int dtype, const void* q, const void* k, co
     if (ds_phase || (mode == kAuto && ds_ok)) {
         p.ds = static_cast<unsigned char*>(workspace) + rows_bytes;
         hipError_t e = hipSuccess;
-        if (mode == kAuto || mode == kDs0) e = sdpa::launch_bwd_rows_f16(p, stream);
-        if (e == hipSuccess && (mode == kAuto || mode == kDs1)) e = sdpa::launch_bwd_dkdv_f16_split(p, stream);
-        if (e == hipSuccess && (mode == kAuto || mode == kDs2)) e = sdpa::launch_bwd_dq_ds_f16(p, stream);
+        const bool f16 = dtype == SDPA_DTYPE_F16;
+        if (mode == kAuto || mode == kDs0)
+            e = f16 ? sdpa::launch_bwd_rows_f16(p, stream) : sdpa::launch_bwd_rows_f32(p, stream);
+        if (e == hipSuccess && (mode == kAuto || mode == kDs1))
+            e = f16 ? sdpa::launch_bwd_dkdv_f16_split(p, stream)
+                    : sdpa::launch_bwd(p, sdpa::DType::F32, true, sdpa::kBwdDkDv, stream);
+        if (e == hipSuccess && (mode == kAuto || mode == kDs2))
+            e = f16 ? sdpa::launch_bwd_dq_ds_f16(p, stream) : sdpa::launch_bwd_dq_ds_f32(p, stream);
         return hip_status(e);
     }
     const int ph = mode == kAuto ? (sdpa::kBwdDq | sdpa::kBwdDkDv) : phases;

@@ -67,10 +67,14 @@ hipError_t launch_bwd_dq_f16_dma(const BwdParams& p, hipStream_t stream);
 hipError_t launch_bwd_dkdv_f16_split(const BwdParams& p, hipStream_t stream);
 
 // dS path of the fp16 DMA backward (sdpa_f16_dq_ds.hip), for the shapes the
-// split dK/dV kernel serves: the row values (stats2, delta), then
+// split dK/dV kernels serve: the row values (stats2, delta), then
 // launch_bwd_dkdv_f16_split with p.ds, then dQ from the stored dS'.
 inline bool bwd_ds_shape(int D_qk, int D_v) { return D_qk > 64 || D_v > 64; }
 hipError_t launch_bwd_rows_f16(const BwdParams& p, hipStream_t stream);
 hipError_t launch_bwd_dq_ds_f16(const BwdParams& p, hipStream_t stream);
+// The same path for fp32 (sdpa_f32_dq_ds.hip; its dK/dV phase is launch_bwd
+// with p.ds set, which runs the fp32 split dK/dV kernel storing dS).
+hipError_t launch_bwd_rows_f32(const BwdParams& p, hipStream_t stream);
+hipError_t launch_bwd_dq_ds_f32(const BwdParams& p, hipStream_t stream);
 
 }  // namespace sdpa

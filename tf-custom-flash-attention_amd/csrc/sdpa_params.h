@@ -56,33 +56,43 @@ struct BwdParams {
     AttnScalars c;
 };
 
-// Layout of the stored dS' of the fp16 dS path.  The dK/dV kernel walks key
-// tiles of 128 keys; under the causal mask key tile kt visits the query
-// blocks (64 queries) qb >= qbb(kt) = min(128 kt, S_q) / 64, else all of
-// them.  Each visited (kt, qb) is a 16 KB chunk, and the chunks of a batch
-// row follow each other kt-major, qb-minor.  Inside a chunk: two 32-query
-// sub-tiles t of 8 KB, each four 2 KB key groups (32 keys), each four 512-byte
-// planes p of 32 slots of 16 bytes.  Slot slot(key, p) of plane p = 2 j + h
-// holds the key's dS' at query positions 16 h + 8 j .. + 7: one store j of the
-// dK/dV lane 32 h + key, so each store instruction writes 1 KB in whole 64-byte
-// runs of four lanes.  The key order inside a plane (key ^ 4 p) puts the four
-// planes' rows 0-3 in different LDS banks, for the dQ kernel's transposed read
-// of the group copied as it lies.  The 32 query positions are in the order the
-// dK/dV kernel's lanes hold them: position i is query
-// 8 ((i >> 2) & 3) + 4 (i >> 4) + (i & 3) of the sub-tile.
-struct DsLayout {
-    static constexpr int KT = 128, QBK = 64, CHUNK = 16384;
+// Layout of the stored dS of the dS path.  The dK/dV kernel walks key tiles
+// of 128 keys and query blocks of QBK queries (64 in the fp16 kernel, 32 in
+// the fp32 one); under the causal mask key tile kt visits the query blocks
+// qb >= qbb(kt) = min(128 kt, S_q) / QBK, else all of them.  Each visited
+// (kt, qb) is a 16 KB chunk, and the chunks of a batch row follow each other
+// kt-major, qb-minor.
+//
+// fp16 (DsLayout, QBK 64, dS' = dS (1-p)): inside a chunk, two 32-query
+// sub-tiles t of 8 KB, each four 2 KB key groups (32 keys), each four
+// 512-byte planes p of 32 slots of 16 bytes.  Slot slot(key, p) of plane
+// p = 2 j + h holds the key's dS' at query positions 16 h + 8 j .. + 7: one
+// store j of the dK/dV lane 32 h + key, so each store instruction writes 1 KB
+// in whole 64-byte runs of four lanes.  The key order inside a plane
+// (key ^ 4 p) puts the four planes' rows 0-3 in different LDS banks, for the
+// dQ kernel's transposed read of the group copied as it lies.
+//
+// fp32 (DsLayout32, QBK 32, dS): inside a chunk, 128 key rows of 32 floats,
+// a lane's 16 values (query positions 16 h + 0 .. 15) at 64 h bytes of its
+// key's row.
+//
+// In both, the 32 query positions of a sub-tile are in the order the dK/dV
+// kernel's lanes hold them: position i is query 8 ((i >> 2) & 3) + 4 (i >> 4)
+// + (i & 3) of the sub-tile.
+template <int QBK_>
+struct DsLayoutT {
+    static constexpr int KT = 128, QBK = QBK_, R = KT / QBK, CHUNK = 16384;
     int S_q, QB, F, tiles;
     bool causal;
-    __host__ __device__ DsLayout(int S_q_, int S_kv, bool causal_)
+    __host__ __device__ DsLayoutT(int S_q_, int S_kv, bool causal_)
         : S_q(S_q_), QB((S_q_ + QBK - 1) / QBK), F(S_q_ / QBK), tiles((S_kv + KT - 1) / KT), causal(causal_) {}
     // first query block key tile kt visits
-    __host__ __device__ int qbb(int kt) const { return !causal ? 0 : ((long long)KT * kt <= S_q ? 2 * kt : F); }
+    __host__ __device__ int qbb(int kt) const { return !causal ? 0 : ((long long)KT * kt <= S_q ? R * kt : F); }
     // chunks of the key tiles before kt
     __host__ __device__ long long prefix(int kt) const {
         if (!causal) return (long long)kt * QB;
         const long long J = kt < S_q / KT + 1 ? kt : S_q / KT + 1;  // tiles j < kt with 128 j <= S_q
-        return J * QB - J * (J - 1) + (long long)(kt - J) * (QB - F);
+        return J * QB - R * (J * (J - 1) / 2) + (long long)(kt - J) * (QB - F);
     }
     __host__ __device__ long long per_row() const { return prefix(tiles); }
     // byte offset of chunk (b, kt, qb), qb >= qbb(kt)
@@ -90,8 +100,10 @@ struct DsLayout {
         return ((size_t)b * (size_t)per_row() + (size_t)prefix(kt) + (size_t)(qb - qbb(kt))) * CHUNK;
     }
     __host__ __device__ size_t bytes(int B) const { return (size_t)B * (size_t)per_row() * CHUNK; }
-    // byte offset of (key, plane p) inside its 2 KB key group
+    // fp16: byte offset of (key, plane p) inside its 2 KB key group
     __host__ __device__ static constexpr int slot(int key, int p) { return p * 512 + (key ^ (4 * p)) * 16; }
 };
+using DsLayout = DsLayoutT<64>;
+using DsLayout32 = DsLayoutT<32>;
 
 }  // namespace sdpa

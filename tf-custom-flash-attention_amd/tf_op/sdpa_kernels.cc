@@ -91,7 +91,7 @@ struct Backend<GPUDevice> {
                       int S_kv, int D_qk, int D_v, float scale, float dropout, bool causal, uint64 seed,
                       uint64 offset) {
         // Workspace from TF's allocator: the dS path's (the per-row values and
-        // the stored dS, fp16 at a feature size over 64) when it can be had,
+        // the stored dS, fp16 or fp32 at a feature size over 64) when it can be had,
         // else the per-row one (both backward kernels then form dS).
         size_t ws_bytes = sdpa_hip_bwd_workspace_bytes_ds(dt, B, S_q, S_kv, D_qk, D_v, causal ? 1 : 0);
         Tensor ws;
