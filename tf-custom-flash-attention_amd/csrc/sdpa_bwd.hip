@@ -284,6 +284,7 @@ void sdpa_bwd_dkdv_f16_kernel(const BwdParams p) {
 #pragma unroll
     for (int ks = 0; ks < DV / 16; ++ks)
         vreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, VEC>(Vb, my_k, S_kv, 16 * ks + 8 * hh, D_v, D_v));
+    prologue_loads_landed();
 
     // Queries below k0 see none of these keys under the causal mask.
     const int q_begin = causal ? (min(k0, S_q) / BQ) * BQ : 0;
@@ -707,6 +708,7 @@ void sdpa_bwd_dkdv_f32_kernel(const BwdParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) vf[4 * u + e] = f[e];
     }
+    prologue_loads_landed();
 
     const int q_begin = causal ? (min(k0, S_q) / BQ) * BQ : 0;
     const int nblk = (S_q - q_begin + BQ - 1) / BQ;
@@ -953,6 +955,7 @@ void sdpa_bwd_dkdv_f32_split_kernel(const BwdParams p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) kf[4 * u + e] = f[e];
         }
+        prologue_loads_landed();
         const uint64_t st_base = DROP ? lcg_state(p.c.seed_offset, (uint64_t)b * S_q + 4 * hh, (uint64_t)S_kv, my_k) : 0;
         const uint64_t row_step = (uint64_t)S_kv * kLcgMul;
         const uint32_t thr = p.c.drop_threshold;
@@ -1045,6 +1048,7 @@ void sdpa_bwd_dkdv_f32_split_kernel(const BwdParams p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) vf[4 * u + e] = f[e];
         }
+        prologue_loads_landed();
         floatx16 dkacc[DQK / 32];
 #pragma unroll
         for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};

@@ -118,6 +118,14 @@ __device__ __forceinline__ bool lcg_keep(uint64_t state, uint32_t threshold) {
     return (uint32_t)(state >> 32) >= threshold;
 }
 
+// s_waitcnt vmcnt(0) after the operand rows a kernel loads into registers
+// once, before its loop.  Without it the compiler's wait analysis, which
+// merges the loop's entry state with its back edge, keeps those loads
+// pending in every iteration and puts a vmcnt(0) before the loop's first use
+// of them, which then also waits for every copy and store the iteration has
+// in flight.
+__device__ __forceinline__ void prologue_loads_landed() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Wave-uniform "any lane" test.
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 

@@ -143,20 +143,27 @@ void sdpa_bwd_dq_ds_f32_kernel(const BwdParams p, const int win) {
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx16{};
     // lane terms of the reads: K[2 p + hh][32 dt + l32] and dS[2 p + hh][l32]
     const int krow_sw = hh ? SWZ : 0;
+    // All of a step's operands are read first (BN / 2 (1 + NDT) floats per
+    // lane), so that each MFMA finds its operands landed instead of waiting
+    // out the LDS latency of a read issued just before it.
     auto step_mfma = [&](uint32_t so) {
         const float* Ks = reinterpret_cast<const float*>(smem + so);
         const float* Ss = reinterpret_cast<const float*>(smem + so + Cfg::KB + Cfg::SB * wave);
+        float bv[BN / 2], av[BN / 2][NDT];
 #pragma unroll
         for (int pr = 0; pr < BN / 2; ++pr) {
             const int r = 2 * pr + hh;
-            const float bv = Ss[r * 32 + l32];
+            bv[pr] = Ss[r * 32 + l32];
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
                 const int c = (8 * dt + (l32 >> 2)) ^ krow_sw;
-                const float av = Ks[r * DQK + 4 * c + (l32 & 3)];
-                acc[dt] = mfma_f32(av, bv, acc[dt]);
+                av[pr][dt] = Ks[r * DQK + 4 * c + (l32 & 3)];
             }
         }
+#pragma unroll
+        for (int pr = 0; pr < BN / 2; ++pr)
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma_f32(av[pr][dt], bv[pr], acc[dt]);
     };
 
     if (nsteps > 0) issue(0);

@@ -88,6 +88,7 @@ void sdpa_fwd_f16_kernel(const FwdParams p) {
         const uint4 c = load_row_chunk<half_t, VEC>(Qb, my_q, S_q, 16 * ks + 8 * hh, D_qk, D_qk);
         qreg[ks] = __builtin_bit_cast(half8, c);
     }
+    prologue_loads_landed();
 
     const int kv_end = causal ? min(S_kv, q0 + BM) : S_kv;
     const int nblk = (kv_end + BN - 1) / BN;
@@ -325,6 +326,7 @@ void sdpa_fwd_f32_kernel(const FwdParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) qf[4 * u + e] = f[e];
     }
+    prologue_loads_landed();
 
     const int kv_end = causal ? min(S_kv, q0 + BM) : S_kv;
     const int nblk = (kv_end + BN - 1) / BN;
