@@ -89,6 +89,7 @@ void sdpa_bwd_dkdv_f16_dma_kernel(const BwdParams p, const int win) {
 #pragma unroll
     for (int ks = 0; ks < DV / 16; ++ks)
         vreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Vb, my_k, S_kv, 16 * ks + 8 * hh, D_v, D_v));
+    prologue_loads_landed();
 
     // Queries below k0 see none of these keys under the causal mask.  The
     // query blocks are walked top-down: every key tile of a batch row starts

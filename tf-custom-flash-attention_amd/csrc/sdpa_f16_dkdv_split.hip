@@ -108,6 +108,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
 #pragma unroll
         for (int ks = 0; ks < DQK / 16; ++ks)
             kreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Kb, my_k, S_kv, 16 * ks + 8 * hh, D_qk, D_qk));
+        prologue_loads_landed();
         const float sl2 = p.c.scale_log2;
         // Dropout: st(q, key) = st(4 hh, key) + q * S_kv * A.
         const uint64_t st_lane = DROP ? lcg_state(p.c.seed_offset, (uint64_t)b * S_q + 4 * hh, (uint64_t)S_kv, my_k) : 0;
@@ -344,6 +345,7 @@ void sdpa_bwd_dkdv_f16_split_kernel(const BwdParams p, const int win) {
 #pragma unroll
         for (int ks = 0; ks < DV / 16; ++ks)
             vreg[ks] = __builtin_bit_cast(half8, load_row_chunk<half_t, true>(Vb, my_k, S_kv, 16 * ks + 8 * hh, D_v, D_v));
+        prologue_loads_landed();
         // With dropout the factor 1/(1-p) is taken out of dS: this role forms
         //   dS' = P (keep ? dP - delta' : -delta'),  delta' = delta / (1/(1-p))
         // (the reference's D_i / dp_inverse_scale, sdpa/sdpa_cpu.cc:428) and
