@@ -248,6 +248,25 @@ def test_ds_stored_and_dq_product(pkg, O, shape):
     assert err_dq <= 2e-3 * max(1.0, float(np.abs(dq_host).max()))
 
 
+def _slot32(key, pos):
+    """Byte offset of (key, query position) inside a stored fp32 key group of
+    32 keys (csrc/sdpa_params.h, DsLayout32::slot32): quarter u = the store
+    holding positions 16 h + 4 u .. + 3, half h, the key's 16-byte slot at
+    key ^ (u + 4 h)."""
+    u, h = (pos >> 2) & 3, pos >> 4
+    return 1024 * u + 512 * h + 16 * (key ^ (u + 4 * h)) + 4 * (pos & 3)
+
+
+def _ds32_gather():
+    """[128 keys, 32 positions] float indices into a 16 KB fp32 chunk."""
+    g = np.empty((128, 32), np.int64)
+    for key in range(128):
+        for pos in range(32):
+            g[key, pos] = ((key // 32) * 4096 + _slot32(key % 32, pos)) // 4
+    assert np.unique(g).size == 4096
+    return g
+
+
 def _ds_layout32(S_q, S_kv, causal):
     """(kt, qb) -> chunk index within a batch row, and chunks per row, for the
     fp32 split dK/dV kernel: key tiles of 128, query blocks of 32 (its
@@ -266,8 +285,9 @@ def _ds_layout32(S_q, S_kv, causal):
                          ids=["f32_causal_d128_S200", "f32_cross_128x64", "f32_causal_100x36"])
 def test_ds32_stored_and_dq_product(pkg, O, shape):
     """fp32: the stored dS against a float64 dS of the same inputs at every
-    stored position (key rows of 32 floats, a lane's 16 values at query
-    positions 16 h + r), and phase 2's dQ against scale * (stored dS) K."""
+    stored position (decoded through _slot32: each key group of 32 keys as
+    four 1 KB stores of 16-byte slots), and phase 2's dQ against
+    scale * (stored dS) K."""
     B, S_q, S_kv, D_qk, D_v, causal = shape
     c = Cfg("ds32_diag", "f32", B, S_q, S_kv, D_qk, D_v, causal, 0.0, D_qk ** -0.5, 4, 1)
     from _common import make_inputs
@@ -290,7 +310,7 @@ def test_ds32_stored_and_dq_product(pkg, O, shape):
     raw = ws[rows:].cpu().numpy().view(np.float32).astype(np.float64)
     idx, per_row = _ds_layout32(S_q, S_kv, causal)
     assert raw.size == B * per_row * 4096
-    chunks = raw.reshape(B, per_row, 128, 32)  # [chunk][key][position]
+    chunks = raw.reshape(B, per_row, 4096)[:, :, _ds32_gather()]  # [chunk][key][position]
     pi = _perm()
     f64 = lambda a: a.astype(np.float64)
     o_h, s_h = f64(_np(o)), f64(_np(s))

@@ -1053,9 +1053,9 @@ void sdpa_bwd_dkdv_f32_split_kernel(const BwdParams p) {
 #pragma unroll
         for (int dt = 0; dt < DQK / 32; ++dt) dkacc[dt] = floatx16{};
         // dS path: this key group's dS of each visited block goes to its
-        // chunk (DsLayout32), the lane's 16 values at query positions
-        // 16 hh + r of its key row; zero for keys past S_kv (the dQ kernel
-        // reads them unmasked)
+        // chunk (DsLayout32): the lane's 16 values, query positions 16 hh + r,
+        // as four 16-byte slots, one per store, each store 1 KB whole; zero
+        // for keys past S_kv (the dQ kernel reads them unmasked)
         const DsLayout32 dsl(S_q, S_kv, causal);
 
         for (int n = 0; n <= nblk; ++n) {
@@ -1094,14 +1094,14 @@ void sdpa_bwd_dkdv_f32_split_kernel(const BwdParams p) {
                     }
                 }
                 if constexpr (DS) {
-                    float* dst = reinterpret_cast<float*>(static_cast<unsigned char*>(p.ds) +
-                                                          dsl.offset(b, kt, q0 / BQ) + kw * 4096 + l32 * 128 + hh * 64);
+                    unsigned char* grp = static_cast<unsigned char*>(p.ds) + dsl.offset(b, kt, q0 / BQ) + kw * 4096;
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
                         floatx4 v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] = key_ok ? dpacc[4 * u + e] : 0.f;
-                        __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(dst + 4 * u));
+                        __builtin_nontemporal_store(
+                            v, reinterpret_cast<floatx4*>(grp + DsLayout32::slot32(l32, 16 * hh + 4 * u)));
                     }
                 }
 #pragma unroll

@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void sdpa_bwd_rows_f32_kernel(const BwdParams 
 // dQ from the stored dS.  Four waves of 32 queries (128 per workgroup): a
 // wave owns one stored query block.  Key steps of 32 (one stored key group)
 // through two LDS stages of the K tile (32 rows of D_qk floats, row-major)
-// and each wave's dS tile (32 key rows of 32 floats, as stored).  Each
+// and each wave's dS tile (one stored 4 KB key group, copied as it lies).  Each
 // v_mfma_f32_32x32x2_f32 takes a key pair: lane (l32, hh) reads
 // K[2 p + hh][32 dt + l32] (the A operand K^T) and dS[2 p + hh][l32] (the B
 // operand dS^T, lane = query position), so the accumulators hold dQ^T with
@@ -83,7 +83,7 @@ template <int DQK, bool CAUSAL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sdpa_bwd_dq_ds_f32_kernel(const BwdParams p, const int win) {
     using Cfg = DqDs32Cfg<DQK>;
-    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, NW = Cfg::NW, NSTAGE = Cfg::NSTAGE, CPW = Cfg::CPW;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, LK = Cfg::LK, NSTAGE = Cfg::NSTAGE, CPW = Cfg::CPW;
     constexpr int NDT = DQK / 32;
     static_assert(DsLayout32::KT % BN == 0 && BN == DsLayout32::QBK, "steps tile the stored key groups");
     static_assert(NSTAGE == 2, "one step of copies ahead");
@@ -141,19 +141,25 @@ void sdpa_bwd_dq_ds_f32_kernel(const BwdParams p, const int win) {
     floatx16 acc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx16{};
-    // lane terms of the reads: K[2 p + hh][32 dt + l32] and dS[2 p + hh][l32]
+    // lane terms of the reads: K[2 p + hh][32 dt + l32] and dS[2 p + hh][l32].
+    // dS sits at DsLayout32::slot32(2 p + hh, l32); for p = 4 i + j its key
+    // slot is 8 i + ((2 j + hh) ^ (u + 4 h)) (the XOR term stays below 8), so
+    // one lane base per j and the immediate 128 i.
     const int krow_sw = hh ? SWZ : 0;
+    int sbase[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sbase[j] = DsLayout32::slot32(2 * j + hh, l32);
     // All of a step's operands are read first (BN / 2 (1 + NDT) floats per
     // lane), so that each MFMA finds its operands landed instead of waiting
     // out the LDS latency of a read issued just before it.
     auto step_mfma = [&](uint32_t so) {
         const float* Ks = reinterpret_cast<const float*>(smem + so);
-        const float* Ss = reinterpret_cast<const float*>(smem + so + Cfg::KB + Cfg::SB * wave);
+        const unsigned char* Ss = smem + so + Cfg::KB + Cfg::SB * wave;
         float bv[BN / 2], av[BN / 2][NDT];
 #pragma unroll
         for (int pr = 0; pr < BN / 2; ++pr) {
             const int r = 2 * pr + hh;
-            bv[pr] = Ss[r * 32 + l32];
+            bv[pr] = *reinterpret_cast<const float*>(Ss + sbase[pr & 3] + 128 * (pr >> 2));
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
                 const int c = (8 * dt + (l32 >> 2)) ^ krow_sw;

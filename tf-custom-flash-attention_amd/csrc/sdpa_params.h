@@ -72,9 +72,13 @@ struct BwdParams {
 // (key ^ 4 p) puts the four planes' rows 0-3 in different LDS banks, for the
 // dQ kernel's transposed read of the group copied as it lies.
 //
-// fp32 (DsLayout32, QBK 32, dS): inside a chunk, 128 key rows of 32 floats,
-// a lane's 16 values (query positions 16 h + 0 .. 15) at 64 h bytes of its
-// key's row.
+// fp32 (DsLayout32, QBK 32, dS): inside a chunk, four 4 KB key groups (32
+// keys), each four 1 KB quarters u, each two 512-byte halves h of 32 slots of
+// 16 bytes.  Slot slot32(key, pos) of quarter u, half h holds the key's dS at
+// query positions 16 h + 4 u .. + 3: store u of the dK/dV lane 32 h + key, so
+// each store instruction writes 1 KB whole.  The key order inside a half
+// (key ^ (u + 4 h)) puts the eight (u, h) slots of one key row in different
+// LDS banks, for the dQ kernel's read of a key row by 32 lanes.
 //
 // In both, the 32 query positions of a sub-tile are in the order the dK/dV
 // kernel's lanes hold them: position i is query 8 ((i >> 2) & 3) + 4 (i >> 4)
@@ -102,6 +106,11 @@ struct DsLayoutT {
     __host__ __device__ size_t bytes(int B) const { return (size_t)B * (size_t)per_row() * CHUNK; }
     // fp16: byte offset of (key, plane p) inside its 2 KB key group
     __host__ __device__ static constexpr int slot(int key, int p) { return p * 512 + (key ^ (4 * p)) * 16; }
+    // fp32: byte offset of (key, query position) inside its 4 KB key group
+    __host__ __device__ static constexpr int slot32(int key, int pos) {
+        return 1024 * ((pos >> 2) & 3) + 512 * (pos >> 4) + 16 * (key ^ (((pos >> 2) & 3) + 4 * (pos >> 4))) +
+               4 * (pos & 3);
+    }
 };
 using DsLayout = DsLayoutT<64>;
 using DsLayout32 = DsLayoutT<32>;
