@@ -142,7 +142,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one MI355X only; multi-GPU runs are not part of "
-              "it (the op shards over the batch with offset += b0*S_q*S_kv, see DESIGN.md)",
+              "it (the op shards over the batch with offset += b0*S_q*S_kv)",
               file=sys.stderr)
         sys.exit(2)
 

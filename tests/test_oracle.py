@@ -1,9 +1,10 @@
 """Pins the CPU oracle (oracle/sdpa_oracle.cc, restating sdpa/sdpa_cpu.cc)
 before it is trusted as the parity checker of the HIP kernels.
 
-* dropout hash: SURVEY-derived known answers, the golden JSON written by an
-  independent Python restatement, the linearity of the counter, and an
-  exhaustive check over all 2^32 hash words that the reference's float
+* dropout hash: known answers of the counter's closed form
+  ((seed + offset + (b S_q + i) S_kv + j) A + C mod 2^64, high word), the
+  golden JSON written by an independent Python restatement, the linearity
+  of the counter, and an exhaustive check over all 2^32 hash words that the reference's float
   predicate u < p equals the integer threshold used by the kernels;
 * attention math: float64 dense attention fixtures (tests/golden), finite
   differences of the dense forward (pinning the closed-form gradients those
@@ -32,7 +33,7 @@ def golden_dense():
 # ---------------------------------------------------------------------------
 # dropout hash
 # ---------------------------------------------------------------------------
-SURVEY_ANSWERS = [
+KNOWN_ANSWERS = [
     ((42, 1000, 0, 0, 0, 400, 400), 0x91995BE0),
     ((42, 1000, 0, 0, 1, 400, 400), 0xE9EB500D),
     ((42, 1000, 0, 1, 0, 400, 400), 0x91A6E2A8),
@@ -43,7 +44,7 @@ SURVEY_ANSWERS = [
 ]
 
 
-@pytest.mark.parametrize("args,want", SURVEY_ANSWERS)
+@pytest.mark.parametrize("args,want", KNOWN_ANSWERS)
 def test_rng_known_answers(O, args, want):
     assert O.rng_bits(*args) == want
 
