@@ -47,6 +47,10 @@ CASES = [
     Cfg("ds32_cross_64x128_p0.2", "f32", 2, 257, 130, 64, 128, False, 0.2, 64 ** -0.5, 1, 2),
     Cfg("ds32_causal_100x36", "f32", 2, 161, 161, 100, 36, True, 0.05, 100 ** -0.5, 7, 8),
     Cfg("ds32_causal_drop_all", "f32", 2, 96, 96, 128, 128, True, 1.5, 128 ** -0.5, 2, 6),
+    # a 32-wide D_qk beside a 128-wide D_v: dQ from dS with a 32-feature K
+    # tile (one copy per wave, no row swizzle)
+    Cfg("ds_causal_32x128", "f16", 2, 190, 190, 32, 128, True, 0.1, 32 ** -0.5, 6, 1),
+    Cfg("ds32_cross_32x128", "f32", 2, 75, 260, 32, 128, False, 0.1, 32 ** -0.5, 8, 2),
 ]
 
 
