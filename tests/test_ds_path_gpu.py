@@ -51,6 +51,9 @@ CASES = [
     # tile (one copy per wave, no row swizzle)
     Cfg("ds_causal_32x128", "f16", 2, 190, 190, 32, 128, True, 0.1, 32 ** -0.5, 6, 1),
     Cfg("ds32_cross_32x128", "f32", 2, 75, 260, 32, 128, False, 0.1, 32 ** -0.5, 8, 2),
+    # fp32 with a narrow V side (the split dK/dV kernel's <128, 32> instantiation)
+    Cfg("ds32_cross_128x16", "f32", 2, 140, 333, 128, 16, False, 0.1, 128 ** -0.5, 9, 4),
+    Cfg("ds32_causal_96x32", "f32", 2, 170, 170, 96, 32, True, 0.0, 96 ** -0.5, 10, 5),
 ]
 
 
