@@ -271,10 +271,50 @@ def _random_cases(n=24, seed=2024):
 RANDOM = _random_cases()
 
 
+def _random_ds_cases(n=40, seed=77):
+    """Seeded shapes that take the backward's dS path (fp16 or fp32, one side
+    over 64 and both 16-byte aligned: multiples of 8 fp16 / 4 fp32 elements),
+    with D_qk >= 16 so that the scale keeps the fp16 gradients where one ulp
+    is inside the 1e-2 gate."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        dt = "f32" if rng.random() < 0.4 else "f16"
+        w = 8 if dt == "f16" else 4
+        wide = [x for x in (72, 80, 96, 100, 120, 128) if x % w == 0]
+        any_w = [x for x in (16, 24, 32, 40, 48, 64, 72, 96, 128) if x % w == 0]
+        D_qk, D_v = int(rng.choice(any_w)), int(rng.choice(any_w))
+        if D_qk <= 64 and D_v <= 64:
+            if rng.random() < 0.5:
+                D_qk = int(rng.choice(wide))
+            else:
+                D_v = int(rng.choice(wide))
+        causal = bool(rng.integers(0, 2))
+        S_q = int(rng.integers(1, 700))
+        S_kv = S_q if causal else int(rng.integers(1, 700))
+        p = float(rng.choice([0.0, 0.1, 0.3, 1.5]))
+        seed_, off = int(rng.integers(0, 2**63)), int(rng.integers(0, 2**40))
+        cases.append((dt, int(rng.integers(1, 4)), S_q, S_kv, D_qk, D_v, causal, p, seed_, off))
+    return cases
+
+
+RANDOM_DS = _random_ds_cases()
+
+
 @pytest.mark.parametrize("case", RANDOM, ids=[f"r{i}-" + "-".join(map(str, e[:8])) for i, e in enumerate(RANDOM)])
 def test_random_shapes(pkg, O, case):
     dt, B, S_q, S_kv, D_qk, D_v, causal, p, seed_, off = case
     c = Cfg(f"rand_{dt}_{B}x{S_q}x{S_kv}_{D_qk}_{D_v}", dt, B, S_q, S_kv, D_qk, D_v, causal, p,
+            D_qk ** -0.5, seed=seed_, offset=off)
+    run_and_check(pkg, O, c, fp32_sum_allowance=True)
+
+
+@pytest.mark.parametrize("case", RANDOM_DS, ids=[f"ds{i}-" + "-".join(map(str, e[:8])) for i, e in enumerate(RANDOM_DS)])
+def test_random_ds_path_shapes(pkg, O, case):
+    """Random shapes on the backward's dS path (the default workspace of
+    pkg.sdpa_grad) against the oracle."""
+    dt, B, S_q, S_kv, D_qk, D_v, causal, p, seed_, off = case
+    c = Cfg(f"rds_{dt}_{B}x{S_q}x{S_kv}_{D_qk}_{D_v}", dt, B, S_q, S_kv, D_qk, D_v, causal, p,
             D_qk ** -0.5, seed=seed_, offset=off)
     run_and_check(pkg, O, c, fp32_sum_allowance=True)
 
