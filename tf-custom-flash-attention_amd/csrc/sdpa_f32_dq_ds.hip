@@ -142,9 +142,10 @@ void sdpa_bwd_dq_ds_f32_kernel(const BwdParams p, const int win) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx16{};
     // lane terms of the reads: K[2 p + hh][32 dt + l32] and dS[2 p + hh][l32].
-    // dS sits at DsLayout32::slot32(2 p + hh, l32); for p = 4 i + j its key
-    // slot is 8 i + ((2 j + hh) ^ (u + 4 h)) (the XOR term stays below 8), so
-    // one lane base per j and the immediate 128 i.
+    // dS sits at DsLayout32::slot32(2 p + hh, l32), with u = (l32 >> 2) & 3
+    // and h = l32 >> 4 from the lane's query position; for p = 4 i + j its
+    // key slot is 8 i + ((2 j + hh) ^ (u + 4 h)) (the XOR term stays below 8),
+    // so one lane base per j and the immediate 128 i.
     const int krow_sw = hh ? SWZ : 0;
     int sbase[4];
 #pragma unroll
